@@ -1,0 +1,228 @@
+/*
+ * dlmk.h -- C ABI of the MI355X (gfx950) paged KV-cache library, libdlmk.so.
+ *
+ * Drop-in for dlm's paged KV-cache path (vedantnimbarte/dlm).  The reference
+ * keeps KV bookkeeping in Rust (src/cache/paged.rs) and reaches the GPU through
+ * one extern "C" entry, dlm_decode_block (src/gpu/kernels.cu:313-392, declared
+ * in src/forward/gpu.rs:34-64), whose KV part is a contiguous copy_kernel append
+ * (kernels.cu:361-363) and attention_kernel (kernels.cu:365-366).  This header
+ * replaces those with paged equivalents plus the block-table store itself.
+ *
+ * Conventions (following dlm_decode_block, kernels.cu:378-391):
+ *   - every function returns int: 0 on success, a positive hipError_t from the
+ *     HIP runtime, or a negative DLMK_ERR_* code for an argument/state error;
+ *     dlmk_get_last_error_string() describes the last failure on this thread;
+ *   - device entry points take an explicit hipStream_t (passed as void*; NULL is
+ *     the null stream), only enqueue work, and never synchronise;
+ *   - every buffer is caller-owned; pointers named *_pool, q, out, slot_mapping,
+ *     block_tables, ctx_lens, pairs, block_ids, workspace and staging are device
+ *     pointers; host_* pointers are pinned host memory;
+ *   - no torch types appear anywhere: plain pointers and sizes.
+ *
+ * Physical layout of one layer's pools (both pools hold num_blocks blocks):
+ *   K pool: [num_blocks][num_kv_heads][head_dim / X][block_size][X]
+ *   V pool: [num_blocks][num_kv_heads][head_dim][block_size]
+ * with X = 16 / element bytes (8 for f16/bf16, 4 for f32), so every K row of a
+ * block is a run of 16-byte chunks and one (block, kv head) tile is contiguous.
+ * The logical view is dlm's KvLayerCache layout [pos][kv_head][head_dim]
+ * (src/forward/cpu.rs:802): token p of a sequence lives in block
+ * table[p / block_size] at offset p % block_size.
+ */
+#ifndef DLMK_H
+#define DLMK_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DLMK_ABI_VERSION 1
+
+/* Element types of K/V pools, queries and outputs. */
+enum dlmk_dtype { DLMK_F32 = 0, DLMK_F16 = 1, DLMK_BF16 = 2 };
+
+/* Negative status codes (positive values are hipError_t). */
+#define DLMK_OK 0
+#define DLMK_ERR_INVALID_ARG -1 /* DlmError::ShapeMismatch / InvalidConfig analogue */
+#define DLMK_ERR_KV_EXHAUSTED -2 /* DlmError::KvCacheExhausted, src/error.rs:70-75 */
+#define DLMK_ERR_UNSUPPORTED -3 /* shape/dtype combination with no kernel */
+#define DLMK_ERR_WORKSPACE -4 /* workspace or staging buffer too small */
+#define DLMK_ERR_UNKNOWN_SEQ -5 /* sequence id not present */
+
+/* Library identity and last error (thread-local). */
+int dlmk_abi_version(void);
+const char *dlmk_get_last_error_string(void);
+
+/* ======================================================================== */
+/* Block-table KV store (host bookkeeping).                                 */
+/* Replaces PagedKvCache, src/cache/paged.rs:106-227, with the same LIFO    */
+/* free list, atomic append and error payload, plus an injectable free      */
+/* order, truncate (speculative rollback) and fork (block-copy prefix        */
+/* sharing).  Not thread-safe: one thread drives a cache at a time, as dlm's */
+/* engine thread does (src/forward/gpu.rs:196-200).                         */
+/* ======================================================================== */
+
+/* KvCacheConfig, src/cache/paged.rs:30-40. */
+typedef struct dlmk_kv_cache_config {
+    uint32_t num_layers;
+    uint32_t num_kv_heads;
+    uint32_t head_dim;
+    uint32_t block_size;
+} dlmk_kv_cache_config;
+
+/* KvCacheStats, src/cache/paged.rs:83-92. */
+typedef struct dlmk_kv_cache_stats {
+    uint32_t total_blocks;
+    uint32_t used_blocks;
+    uint32_t free_blocks;
+    uint32_t _pad;
+    uint64_t num_sequences;
+    uint64_t used_tokens;
+    uint64_t capacity_tokens;
+    uint64_t bytes_per_block;
+} dlmk_kv_cache_stats;
+
+/* Payload of DLMK_ERR_KV_EXHAUSTED (DlmError::KvCacheExhausted, error.rs:70-75). */
+typedef struct dlmk_kv_exhausted {
+    uint32_t requested;
+    uint32_t free;
+    uint32_t total;
+} dlmk_kv_exhausted;
+
+typedef struct dlmk_kv_cache dlmk_kv_cache;
+
+/* KvCacheConfig::{bytes_per_token, bytes_per_block, blocks_for_tokens},
+ * src/cache/paged.rs:52-71 (bytes assume 2-byte elements, paged.rs:26). */
+uint64_t dlmk_bytes_per_token(const dlmk_kv_cache_config *cfg);
+uint64_t dlmk_bytes_per_block(const dlmk_kv_cache_config *cfg);
+uint64_t dlmk_blocks_for_tokens(const dlmk_kv_cache_config *cfg, uint64_t tokens);
+
+/* PagedKvCache::new, paged.rs:116-126 (ids handed out 0, 1, 2, ...). */
+dlmk_kv_cache *dlmk_cache_new(const dlmk_kv_cache_config *cfg, uint32_t total_blocks);
+/* PagedKvCache::with_budget, paged.rs:130-134. */
+dlmk_kv_cache *dlmk_cache_with_budget(const dlmk_kv_cache_config *cfg, uint64_t budget_bytes);
+/* Extension: a pool of n blocks handed out in the order order[0], order[1], ...
+ * (a seeded shuffle of the pool); each id in [0, n) exactly once. NULL on error. */
+dlmk_kv_cache *dlmk_cache_new_with_free_order(const dlmk_kv_cache_config *cfg,
+                                              const uint32_t *order, uint32_t n);
+void dlmk_cache_destroy(dlmk_kv_cache *cache);
+
+/* append_tokens, paged.rs:164-190.  Atomic: on DLMK_ERR_KV_EXHAUSTED nothing
+ * changes and *err (if non-NULL) holds {requested, free, total}. */
+int dlmk_cache_append_tokens(dlmk_kv_cache *cache, uint64_t seq_id, uint64_t n,
+                             dlmk_kv_exhausted *err);
+/* free_sequence, paged.rs:193-197 (blocks return in table order; no-op if unknown). */
+void dlmk_cache_free_sequence(dlmk_kv_cache *cache, uint64_t seq_id);
+/* Extension: roll back to new_len tokens; freed tail blocks return last-first,
+ * so re-appending pops the same blocks.  new_len >= len is a no-op. */
+int dlmk_cache_truncate_sequence(dlmk_kv_cache *cache, uint64_t seq_id, uint64_t new_len);
+/* Extension: new sequence dst with a private copy of src's blocks (paged
+ * KvSnapshot clone, src/forward/orchestrator.rs:73-105).  Writes n (src, dst)
+ * block pairs (host int32[n][2]) for dlmk_copy_blocks.  Atomic on exhaustion. */
+int dlmk_cache_fork_sequence(dlmk_kv_cache *cache, uint64_t src_seq, uint64_t dst_seq,
+                             int32_t *pairs, uint32_t pairs_capacity, uint32_t *n_pairs,
+                             dlmk_kv_exhausted *err);
+
+/* sequence_len, paged.rs:200-202 (0 if unknown). */
+uint64_t dlmk_cache_sequence_len(const dlmk_kv_cache *cache, uint64_t seq_id);
+/* block_table, paged.rs:205-207: copies up to cap ids into out (may be NULL)
+ * and returns the table length, or -1 for an unknown sequence. */
+int64_t dlmk_cache_block_table(const dlmk_kv_cache *cache, uint64_t seq_id, uint32_t *out,
+                               uint64_t cap);
+/* num_sequences / stats, paged.rs:210-227 and the pool counters :137-160. */
+uint64_t dlmk_cache_num_sequences(const dlmk_kv_cache *cache);
+void dlmk_cache_stats(const dlmk_kv_cache *cache, dlmk_kv_cache_stats *out);
+/* The free stack bottom-to-top (top is handed out next); returns its length. */
+uint32_t dlmk_cache_free_list(const dlmk_kv_cache *cache, uint32_t *out, uint32_t cap);
+
+/* Device-side views of the books (host arrays, to be uploaded by the caller).
+ * slot_mapping: slots of tokens [start_pos, start_pos+n) of seq_id
+ * (slot = block * block_size + offset); those tokens must already be appended.
+ * block_tables: row s = table of seq_ids[s] padded with 0 to max_blocks;
+ * ctx_lens[s] = its length (DLMK_ERR_INVALID_ARG if a table is longer). */
+int dlmk_cache_slot_mapping(const dlmk_kv_cache *cache, uint64_t seq_id, uint64_t start_pos,
+                            uint64_t n, int64_t *slot_mapping);
+int dlmk_cache_fill_block_tables(const dlmk_kv_cache *cache, const uint64_t *seq_ids,
+                                 uint32_t n_seqs, uint32_t max_blocks, int32_t *block_tables,
+                                 int32_t *ctx_lens);
+
+/* ======================================================================== */
+/* Device entry points (hand-written HIP for gfx950).                       */
+/* ======================================================================== */
+
+/* Paged KV append: replaces copy_kernel x2 at kernels.cu:361-363 (and
+ * KvLayerCache::append, src/forward/cpu.rs:765-795).  k_src/v_src are
+ * [n_tok][num_kv_heads][head_dim]; token i goes to slot_mapping[i].  A negative
+ * slot, or one >= num_blocks * block_size, is skipped.  A bit copy (f32, f16,
+ * bf16).  Per-token decode and per-chunk prefill alike. */
+int dlmk_kv_append(void *stream, void *k_pool, void *v_pool, const void *k_src,
+                   const void *v_src, const int64_t *slot_mapping, int64_t n_tok,
+                   int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
+                   int dtype);
+
+/* Workspace bytes dlmk_paged_decode_attention needs for these bounds. */
+size_t dlmk_paged_attention_workspace_size(int num_seqs, int num_q_per_seq, int num_q_heads,
+                                           int head_dim, int block_size, int max_blocks_per_seq);
+
+/* Paged GQA decode attention: replaces attention_kernel at kernels.cu:210-242
+ * (launched at :365-366) and attention() at src/forward/cpu.rs:1126-1151.
+ *   q   [num_seqs][num_q_per_seq][num_q_heads][head_dim], same dtype as the pools
+ *   out [num_seqs][num_q_per_seq][num_q_heads][head_dim], out_dtype
+ *   block_tables int32 [num_seqs][max_blocks_per_seq], ctx_lens int32 [num_seqs]
+ * Query j of sequence s attends causally to the first
+ * ctx_lens[s] - num_q_per_seq + j + 1 tokens (num_q_per_seq > 1 is the
+ * speculative-verify case; 1 is plain decode); a query with no visible token
+ * gets zeros.  score = dot(q, k) * scale; softmax; out = sum p * v.
+ * Block ids outside [0, num_blocks) are treated as masked tokens; a context
+ * length above max_blocks_per_seq * block_size is clamped to it.
+ * Contexts are split into fixed partitions processed in parallel and merged by
+ * log-sum-exp in a second pass; workspace holds the partials
+ * (>= dlmk_paged_attention_workspace_size bytes, 256-byte aligned). */
+int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const void *q,
+                                const void *k_pool, const void *v_pool, int dtype,
+                                const int32_t *block_tables, const int32_t *ctx_lens,
+                                int num_seqs, int num_q_per_seq, int num_q_heads,
+                                int num_kv_heads, int head_dim, int block_size,
+                                int max_blocks_per_seq, int64_t num_blocks, float scale,
+                                void *workspace, size_t workspace_bytes);
+
+/* Block copy for fork / copy-on-write: for each pairs[i] = (src, dst) (device
+ * int32[n][2]) copy block src to block dst in both pools.  block_bytes is the
+ * size of one block of one pool (num_kv_heads * block_size * head_dim * elem
+ * bytes), a multiple of 16.  Pairs must not chain (no dst is another's src).
+ * Ids outside [0, num_blocks) are skipped. */
+int dlmk_copy_blocks(void *stream, void *k_pool, void *v_pool, const int32_t *pairs, int64_t n,
+                     size_t block_bytes, int64_t num_blocks);
+
+/* Swap gather: staging (device) [n][2][block_bytes] <- (K block, V block) of
+ * block_ids[i].  Swap scatter is the inverse.  Ids outside the pool are skipped. */
+int dlmk_gather_blocks(void *stream, void *staging, const void *k_pool, const void *v_pool,
+                       const int32_t *block_ids, int64_t n, size_t block_bytes,
+                       int64_t num_blocks);
+int dlmk_scatter_blocks(void *stream, void *k_pool, void *v_pool, const void *staging,
+                        const int32_t *block_ids, int64_t n, size_t block_bytes,
+                        int64_t num_blocks);
+
+/* Swap out to / in from pinned host memory: gather into dev_staging, then one
+ * hipMemcpyAsync D2H (swap_out); or one H2D then scatter (swap_in).  host_buf is
+ * [n][2][block_bytes]; dev_staging must hold 2 * n * block_bytes.  The async
+ * copy is the PCIe analogue of dlm's pinned streaming upload
+ * (src/forward/streaming_gpu.rs:139-164; src/gpu/ffi_hip.rs:44-50). */
+int dlmk_swap_out(void *stream, void *host_buf, const void *k_pool, const void *v_pool,
+                  const int32_t *block_ids, int64_t n, size_t block_bytes, int64_t num_blocks,
+                  void *dev_staging, size_t staging_bytes);
+int dlmk_swap_in(void *stream, void *k_pool, void *v_pool, const void *host_buf,
+                 const int32_t *block_ids, int64_t n, size_t block_bytes, int64_t num_blocks,
+                 void *dev_staging, size_t staging_bytes);
+
+/* Pinned host memory, PinnedBuffer (src/memory/pinned.rs:38-112) analogue. */
+int dlmk_alloc_pinned(void **ptr, size_t bytes);
+int dlmk_free_pinned(void *ptr);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DLMK_H */

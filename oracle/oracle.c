@@ -1,0 +1,550 @@
+/*
+ * oracle.c -- CPU restatement of dlm's paged KV-cache path.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This file is the checker that the HIP product
+ * (dlm_amd/, libdlmk.so) is compared against.  Only tests/, the smoke() entry
+ * in __graft_entry__.py and bench.py's cpu_baseline leg may load it.  The
+ * product never links, calls or falls back to anything here.
+ *
+ * Reference: vedantnimbarte/dlm (Rust).  The reference cannot be built in this
+ * image (no Rust toolchain), so oracle/_ref is empty and this restatement is
+ * pinned by the reference's own known-answer tests, closed forms and f64
+ * brute force (tests/test_oracle_*.py).  Each function below cites the
+ * reference code it follows.
+ *
+ * Arithmetic rules kept from the reference (compile with -ffp-contract=off):
+ *   - dot products are a sequential f32 sum of rounded f32 products
+ *     (Iterator::sum over a.map(|(a,b)| a*b), src/forward/cpu.rs:806);
+ *   - V accumulation is `o += w * v`, a rounded multiply then a rounded add
+ *     (src/forward/cpu.rs:829-831);
+ *   - softmax is max -> exp(x-max) -> running sum -> divide when sum > 0
+ *     (src/forward/cpu.rs:945-957), exp = libm expf as Rust's f32::exp.
+ *
+ * Parts with no reference counterpart (physical paging, f16 KV, free-order
+ * injection, truncate, fork, block copy, swap gather/scatter, multi-query
+ * causal verify) are defined here by the contract "paged result == the
+ * reference's contiguous result on the same logical sequence".
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#define ORC_F32 0
+#define ORC_F16 1
+#define ORC_BF16 2
+
+#define ORC_OK 0
+#define ORC_ERR_INVALID -1
+#define ORC_ERR_EXHAUSTED -2
+#define ORC_ERR_UNKNOWN_SEQ -5
+
+/* ------------------------------------------------------------------------ */
+/* Seeded RNG: SplitMix64 as in tests/gpu_parity.rs:30-52.                   */
+/* ------------------------------------------------------------------------ */
+
+uint64_t orc_rng_seed(uint64_t seed) { return seed ^ 0x9E3779B97F4A7C15ull; }
+
+uint64_t orc_rng_next(uint64_t *state) {
+    *state += 0x9E3779B97F4A7C15ull;
+    uint64_t z = *state;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+/* Rng::vec (tests/gpu_parity.rs:44-51): uniform in [-scale, scale) from the top
+ * 24 bits. */
+void orc_rng_uniform(uint64_t seed, float scale, float *out, int64_t n) {
+    uint64_t s = orc_rng_seed(seed);
+    for (int64_t i = 0; i < n; ++i) {
+        float u = (float)(orc_rng_next(&s) >> 40) / (float)(1u << 24);
+        out[i] = (u * 2.0f - 1.0f) * scale;
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* f16 -> f32, exact: src/storage/safetensors.rs:87-108.                     */
+/* ------------------------------------------------------------------------ */
+
+float orc_f16_to_f32(uint16_t h) {
+    unsigned sign = (h >> 15) & 1u, ex = (h >> 10) & 0x1fu, mant = h & 0x3ffu;
+    float val;
+    if (ex == 0)
+        val = (float)mant * ldexpf(1.0f, -24);
+    else if (ex == 0x1f)
+        val = mant == 0 ? INFINITY : NAN;
+    else
+        val = (1.0f + (float)mant / 1024.0f) * ldexpf(1.0f, (int)ex - 15);
+    return sign ? -val : val;
+}
+
+/* bf16 -> f32 is a 16-bit shift (the bf16 pattern is the high half of f32). */
+static float bf16_to_f32(uint16_t h) {
+    uint32_t u = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &u, 4);
+    return f;
+}
+
+static float load_elem(const void *base, int64_t idx, int dtype) {
+    if (dtype == ORC_F32) return ((const float *)base)[idx];
+    if (dtype == ORC_F16) return orc_f16_to_f32(((const uint16_t *)base)[idx]);
+    return bf16_to_f32(((const uint16_t *)base)[idx]);
+}
+
+static int elem_bytes(int dtype) { return dtype == ORC_F32 ? 4 : 2; }
+
+/* ------------------------------------------------------------------------ */
+/* Block geometry: src/cache/paged.rs:23-71.                                 */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    uint32_t num_layers, num_kv_heads, head_dim, block_size;
+} orc_cache_config;
+
+/* KV_DTYPE_BYTES = 2 (paged.rs:26): the budget math always assumes fp16. */
+uint64_t orc_bytes_per_token(const orc_cache_config *c) {
+    return 2ull * c->num_kv_heads * c->head_dim * 2ull * c->num_layers;
+}
+uint64_t orc_bytes_per_block(const orc_cache_config *c) {
+    return orc_bytes_per_token(c) * c->block_size;
+}
+uint64_t orc_blocks_for_tokens(const orc_cache_config *c, uint64_t tokens) {
+    uint64_t bs = c->block_size;
+    return (tokens + bs - 1) / bs; /* u64::div_ceil */
+}
+
+/* ------------------------------------------------------------------------ */
+/* PagedKvCache bookkeeping: src/cache/paged.rs:106-227.                     */
+/* ------------------------------------------------------------------------ */
+
+typedef struct {
+    uint64_t id, length;
+    uint32_t *blocks;
+    uint32_t nblocks, cap;
+} orc_seq;
+
+typedef struct {
+    orc_cache_config cfg;
+    uint32_t total_blocks;
+    uint32_t *free; /* LIFO stack; top = free[nfree-1] */
+    uint32_t nfree;
+    orc_seq *seqs; /* unordered; BTreeMap order is never observable here */
+    uint32_t nseqs, seqcap;
+} orc_cache;
+
+/* PagedKvCache::new (paged.rs:116-126): free = (0..n).rev(), so popping from
+ * the back hands out 0, 1, 2, ... */
+orc_cache *orc_cache_new(const orc_cache_config *cfg, uint32_t total_blocks) {
+    orc_cache *c = (orc_cache *)calloc(1, sizeof(orc_cache));
+    c->cfg = *cfg;
+    if (c->cfg.block_size == 0) c->cfg.block_size = 1; /* block_size.max(1), :46 */
+    c->total_blocks = total_blocks;
+    c->free = (uint32_t *)malloc(sizeof(uint32_t) * (total_blocks ? total_blocks : 1));
+    for (uint32_t i = 0; i < total_blocks; ++i) c->free[i] = total_blocks - 1 - i;
+    c->nfree = total_blocks;
+    return c;
+}
+
+/* Extension (no reference counterpart): blocks are handed out in the order
+ * `order[0], order[1], ...`, i.e. the stack is `order` reversed.  With
+ * order = 0..n it is identical to orc_cache_new. */
+orc_cache *orc_cache_new_with_free_order(const orc_cache_config *cfg, const uint32_t *order,
+                                         uint32_t n) {
+    orc_cache *c = orc_cache_new(cfg, n);
+    for (uint32_t i = 0; i < n; ++i) c->free[i] = order[n - 1 - i];
+    return c;
+}
+
+/* with_budget (paged.rs:130-134). */
+orc_cache *orc_cache_with_budget(const orc_cache_config *cfg, uint64_t budget) {
+    orc_cache_config c2 = *cfg;
+    if (c2.block_size == 0) c2.block_size = 1;
+    uint64_t per = orc_bytes_per_block(&c2);
+    if (per == 0) per = 1;
+    uint64_t n = budget / per;
+    if (n > 0xffffffffull) n = 0xffffffffull;
+    return orc_cache_new(cfg, (uint32_t)n);
+}
+
+void orc_cache_destroy(orc_cache *c) {
+    if (!c) return;
+    for (uint32_t i = 0; i < c->nseqs; ++i) free(c->seqs[i].blocks);
+    free(c->seqs);
+    free(c->free);
+    free(c);
+}
+
+static orc_seq *find_seq(orc_cache *c, uint64_t id) {
+    for (uint32_t i = 0; i < c->nseqs; ++i)
+        if (c->seqs[i].id == id) return &c->seqs[i];
+    return NULL;
+}
+
+static orc_seq *insert_seq(orc_cache *c, uint64_t id) {
+    if (c->nseqs == c->seqcap) {
+        c->seqcap = c->seqcap ? 2 * c->seqcap : 8;
+        c->seqs = (orc_seq *)realloc(c->seqs, sizeof(orc_seq) * c->seqcap);
+    }
+    orc_seq *s = &c->seqs[c->nseqs++];
+    memset(s, 0, sizeof(*s));
+    s->id = id;
+    return s;
+}
+
+static void seq_push(orc_seq *s, uint32_t b) {
+    if (s->nblocks == s->cap) {
+        s->cap = s->cap ? 2 * s->cap : 8;
+        s->blocks = (uint32_t *)realloc(s->blocks, sizeof(uint32_t) * s->cap);
+    }
+    s->blocks[s->nblocks++] = b;
+}
+
+/* append_tokens (paged.rs:164-190): check first, then commit; the error carries
+ * {requested = to_alloc (saturated to u32), free, total}. */
+int orc_cache_append_tokens(orc_cache *c, uint64_t seq_id, uint64_t n, uint32_t err[3]) {
+    orc_seq *s = find_seq(c, seq_id);
+    uint64_t cur_len = s ? s->length : 0, cur_blocks = s ? s->nblocks : 0;
+    uint64_t new_len = cur_len + n;
+    uint64_t needed = orc_blocks_for_tokens(&c->cfg, new_len);
+    uint64_t to_alloc = needed > cur_blocks ? needed - cur_blocks : 0;
+    if (to_alloc > c->nfree) {
+        if (err) {
+            err[0] = to_alloc > 0xffffffffull ? 0xffffffffu : (uint32_t)to_alloc;
+            err[1] = c->nfree;
+            err[2] = c->total_blocks;
+        }
+        return ORC_ERR_EXHAUSTED;
+    }
+    if (!s) s = insert_seq(c, seq_id);
+    for (uint64_t i = 0; i < to_alloc; ++i) seq_push(s, c->free[--c->nfree]);
+    s->length = new_len;
+    return ORC_OK;
+}
+
+static void remove_seq(orc_cache *c, orc_seq *s) {
+    free(s->blocks);
+    *s = c->seqs[--c->nseqs];
+}
+
+/* free_sequence (paged.rs:193-197): blocks go back onto the stack in table
+ * order (Vec::extend), so the last block of the table is handed out next. */
+void orc_cache_free_sequence(orc_cache *c, uint64_t seq_id) {
+    orc_seq *s = find_seq(c, seq_id);
+    if (!s) return;
+    for (uint32_t i = 0; i < s->nblocks; ++i) c->free[c->nfree++] = s->blocks[i];
+    remove_seq(c, s);
+}
+
+/* Extension: roll a sequence back to `new_len` tokens (speculative rejection).
+ * Whole blocks beyond blocks_for_tokens(new_len) return to the stack from the
+ * table's tail backwards, so re-appending the same number of tokens pops the
+ * same physical blocks into the same table slots.  new_len >= len is a no-op. */
+int orc_cache_truncate_sequence(orc_cache *c, uint64_t seq_id, uint64_t new_len) {
+    orc_seq *s = find_seq(c, seq_id);
+    if (!s) return ORC_ERR_UNKNOWN_SEQ;
+    if (new_len >= s->length) return ORC_OK;
+    uint64_t keep = orc_blocks_for_tokens(&c->cfg, new_len);
+    while (s->nblocks > keep) c->free[c->nfree++] = s->blocks[--s->nblocks];
+    s->length = new_len;
+    return ORC_OK;
+}
+
+/* Extension: fork `src` into a new sequence `dst` holding a private copy of
+ * every block (the paged form of KvSnapshot clone + resume,
+ * src/forward/orchestrator.rs:73-105).  Atomic like append_tokens.  Writes
+ * (src_block, dst_block) pairs for the device block copy.  dst must be new. */
+int orc_cache_fork_sequence(orc_cache *c, uint64_t src, uint64_t dst, int32_t *pairs,
+                            uint32_t cap, uint32_t *npairs, uint32_t err[3]) {
+    orc_seq *s = find_seq(c, src);
+    if (!s) return ORC_ERR_UNKNOWN_SEQ;
+    if (find_seq(c, dst)) return ORC_ERR_INVALID;
+    uint32_t need = s->nblocks;
+    if (need > cap) return ORC_ERR_INVALID;
+    if (need > c->nfree) {
+        if (err) {
+            err[0] = need;
+            err[1] = c->nfree;
+            err[2] = c->total_blocks;
+        }
+        return ORC_ERR_EXHAUSTED;
+    }
+    uint64_t len = s->length;
+    uint32_t sidx = (uint32_t)(s - c->seqs);
+    orc_seq *d = insert_seq(c, dst); /* may realloc c->seqs */
+    s = &c->seqs[sidx];
+    for (uint32_t i = 0; i < need; ++i) {
+        uint32_t b = c->free[--c->nfree];
+        seq_push(d, b);
+        pairs[2 * i] = (int32_t)s->blocks[i];
+        pairs[2 * i + 1] = (int32_t)b;
+    }
+    d->length = len;
+    *npairs = need;
+    return ORC_OK;
+}
+
+uint64_t orc_cache_sequence_len(orc_cache *c, uint64_t id) {
+    orc_seq *s = find_seq(c, id);
+    return s ? s->length : 0;
+}
+
+/* block_table (paged.rs:205-207); returns -1 for an unknown sequence. */
+int64_t orc_cache_block_table(orc_cache *c, uint64_t id, uint32_t *out, uint64_t cap) {
+    orc_seq *s = find_seq(c, id);
+    if (!s) return -1;
+    for (uint32_t i = 0; i < s->nblocks && i < cap; ++i) out[i] = s->blocks[i];
+    return s->nblocks;
+}
+
+uint32_t orc_cache_total_blocks(orc_cache *c) { return c->total_blocks; }
+uint32_t orc_cache_free_blocks(orc_cache *c) { return c->nfree; }
+uint32_t orc_cache_used_blocks(orc_cache *c) { return c->total_blocks - c->nfree; }
+uint64_t orc_cache_capacity_tokens(orc_cache *c) {
+    return (uint64_t)c->total_blocks * c->cfg.block_size;
+}
+uint64_t orc_cache_num_sequences(orc_cache *c) { return c->nseqs; }
+uint64_t orc_cache_used_tokens(orc_cache *c) {
+    uint64_t t = 0;
+    for (uint32_t i = 0; i < c->nseqs; ++i) t += c->seqs[i].length;
+    return t;
+}
+/* The free stack, bottom to top, for exact-order comparisons. */
+uint32_t orc_cache_free_list(orc_cache *c, uint32_t *out) {
+    memcpy(out, c->free, sizeof(uint32_t) * c->nfree);
+    return c->nfree;
+}
+
+/* ------------------------------------------------------------------------ */
+/* Contiguous attention: src/forward/cpu.rs:1126-1151 with softmax_inplace   */
+/* (:945-957), key_head_dot / value_head_accumulate for the f32 store        */
+/* (:798-846).  keys/values are the KvLayerCache layout [pos][kv_head][d].   */
+/* ------------------------------------------------------------------------ */
+
+static void softmax_inplace(float *v, int64_t n) {
+    float mx = -INFINITY;
+    for (int64_t i = 0; i < n; ++i) mx = fmaxf(mx, v[i]);
+    float sum = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        v[i] = expf(v[i] - mx);
+        sum += v[i];
+    }
+    if (sum > 0.0f)
+        for (int64_t i = 0; i < n; ++i) v[i] /= sum;
+}
+
+/* `scale` is passed in; dlm computes it as 1.0f / sqrtf((float)d) (:1128). */
+void orc_attention(const float *q, const float *keys, const float *values, int64_t positions,
+                   int num_heads, int num_kv_heads, int head_dim, float scale, float *ctx) {
+    int d = head_dim, group = num_heads / num_kv_heads;
+    int64_t kv_dim = (int64_t)num_kv_heads * d;
+    float *scores = (float *)malloc(sizeof(float) * (positions ? positions : 1));
+    for (int h = 0; h < num_heads; ++h) {
+        int kvh = h / group;
+        const float *qh = q + (int64_t)h * d;
+        for (int64_t p = 0; p < positions; ++p) {
+            const float *k = keys + p * kv_dim + (int64_t)kvh * d;
+            float dot = 0.0f;
+            for (int j = 0; j < d; ++j) dot += qh[j] * k[j];
+            scores[p] = dot * scale;
+        }
+        softmax_inplace(scores, positions);
+        float *out = ctx + (int64_t)h * d;
+        for (int j = 0; j < d; ++j) out[j] = 0.0f;
+        for (int64_t p = 0; p < positions; ++p) {
+            const float *v = values + p * kv_dim + (int64_t)kvh * d;
+            float w = scores[p];
+            for (int j = 0; j < d; ++j) out[j] += w * v[j];
+        }
+    }
+    free(scores);
+}
+
+/* ------------------------------------------------------------------------ */
+/* Physical paging (no reference counterpart; see header).                   */
+/*                                                                           */
+/* Per-layer pools, one for K and one for V, each [num_blocks][Hkv][tile]:   */
+/*   K tile = [d / X][block_size][X]  with X = 16 / elem_bytes (16-byte      */
+/*            chunks of X consecutive dims, token-minor inside a chunk row)  */
+/*   V tile = [d][block_size]         (dims outer, tokens contiguous)        */
+/* The logical view is dlm's [pos][kv_head][d].                              */
+/* ------------------------------------------------------------------------ */
+
+static int64_t k_index(int64_t blk, int kvh, int t, int j, int Hkv, int d, int bs, int X) {
+    return ((blk * Hkv + kvh) * (int64_t)d * bs) + ((int64_t)(j / X) * bs + t) * X + (j % X);
+}
+static int64_t v_index(int64_t blk, int kvh, int t, int j, int Hkv, int d, int bs) {
+    return ((blk * Hkv + kvh) * (int64_t)d * bs) + (int64_t)j * bs + t;
+}
+
+/* Paged append (the physical form of KvLayerCache::append, cpu.rs:765-795 for
+ * the f32 store, where extend_from_slice is a bit copy).  src is
+ * [n_tok][Hkv][d]; slot = block*bs + offset; a negative slot, or one beyond
+ * the pool, is skipped.  Elements are copied as raw bits. */
+void orc_paged_append(void *k_pool, void *v_pool, const void *k_src, const void *v_src,
+                      const int64_t *slots, int64_t n_tok, int Hkv, int d, int bs, int dtype,
+                      int64_t num_blocks) {
+    int eb = elem_bytes(dtype), X = 16 / eb;
+    for (int64_t i = 0; i < n_tok; ++i) {
+        int64_t slot = slots[i];
+        if (slot < 0 || slot >= num_blocks * bs) continue;
+        int64_t blk = slot / bs;
+        int t = (int)(slot % bs);
+        for (int h = 0; h < Hkv; ++h)
+            for (int j = 0; j < d; ++j) {
+                int64_t s = (i * Hkv + h) * (int64_t)d + j;
+                memcpy((char *)k_pool + k_index(blk, h, t, j, Hkv, d, bs, X) * eb,
+                       (const char *)k_src + s * eb, eb);
+                memcpy((char *)v_pool + v_index(blk, h, t, j, Hkv, d, bs) * eb,
+                       (const char *)v_src + s * eb, eb);
+            }
+    }
+}
+
+/* Logical view of the first `ctx` tokens of a sequence as f32 [pos][Hkv][d]
+ * (exact f16/bf16 widening). */
+void orc_paged_gather_logical(const void *k_pool, const void *v_pool, const int32_t *table,
+                              int64_t ctx, int Hkv, int d, int bs, int dtype, float *keys,
+                              float *values) {
+    int X = 16 / elem_bytes(dtype);
+    for (int64_t p = 0; p < ctx; ++p) {
+        int64_t blk = table[p / bs];
+        int t = (int)(p % bs);
+        for (int h = 0; h < Hkv; ++h)
+            for (int j = 0; j < d; ++j) {
+                int64_t o = (p * Hkv + h) * (int64_t)d + j;
+                keys[o] = load_elem(k_pool, k_index(blk, h, t, j, Hkv, d, bs, X), dtype);
+                values[o] = load_elem(v_pool, v_index(blk, h, t, j, Hkv, d, bs), dtype);
+            }
+    }
+}
+
+/* Paged GQA attention: attention() (cpu.rs:1126-1151) with key_head_dot /
+ * value_head_accumulate (:798-846) reading through the block table instead
+ * of a contiguous Vec; same arithmetic order, elements widened exactly to f32.
+ *
+ * q is [B][nq][Hq][d] in `dtype`; out is [B][nq][Hq][d] f32.
+ * Multi-query verify: query j of sequence s attends to the first
+ * ctx_lens[s] - nq + j + 1 tokens (causal over the nq appended drafts).
+ * A query with no visible token gets zeros (softmax of an empty vector). */
+void orc_paged_attention(float *out, const void *q, const void *k_pool, const void *v_pool,
+                         int dtype, const int32_t *tables, const int32_t *ctx_lens, int B,
+                         int nq, int Hq, int Hkv, int d, int bs, int max_blocks, float scale) {
+    int X = 16 / elem_bytes(dtype), group = Hq / Hkv;
+    int64_t maxctx = 0;
+    for (int s = 0; s < B; ++s)
+        if (ctx_lens[s] > maxctx) maxctx = ctx_lens[s];
+    float *scores = (float *)malloc(sizeof(float) * (maxctx ? maxctx : 1));
+    float *qh = (float *)malloc(sizeof(float) * d);
+    for (int s = 0; s < B; ++s) {
+        const int32_t *table = tables + (int64_t)s * max_blocks;
+        for (int qi = 0; qi < nq; ++qi) {
+            int64_t positions = (int64_t)ctx_lens[s] - nq + qi + 1;
+            if (positions < 0) positions = 0;
+            for (int h = 0; h < Hq; ++h) {
+                int kvh = h / group;
+                int64_t row = ((int64_t)s * nq + qi) * Hq + h;
+                for (int j = 0; j < d; ++j) qh[j] = load_elem(q, row * d + j, dtype);
+                for (int64_t p = 0; p < positions; ++p) {
+                    int64_t blk = table[p / bs];
+                    int t = (int)(p % bs);
+                    float dot = 0.0f;
+                    for (int j = 0; j < d; ++j)
+                        dot += qh[j] *
+                               load_elem(k_pool, k_index(blk, kvh, t, j, Hkv, d, bs, X), dtype);
+                    scores[p] = dot * scale;
+                }
+                softmax_inplace(scores, positions);
+                float *o = out + row * d;
+                for (int j = 0; j < d; ++j) o[j] = 0.0f;
+                for (int64_t p = 0; p < positions; ++p) {
+                    int64_t blk = table[p / bs];
+                    int t = (int)(p % bs);
+                    float w = scores[p];
+                    for (int j = 0; j < d; ++j)
+                        o[j] += w * load_elem(v_pool, v_index(blk, kvh, t, j, Hkv, d, bs), dtype);
+                }
+            }
+        }
+    }
+    free(qh);
+    free(scores);
+}
+
+/* Block copy for fork: for each (src, dst) pair, the dst block of both pools
+ * becomes a byte copy of the src block.  Pairs are applied in order. */
+void orc_copy_blocks(void *k_pool, void *v_pool, const int32_t *pairs, int64_t n,
+                     int64_t block_bytes) {
+    for (int64_t i = 0; i < n; ++i) {
+        int64_t s = pairs[2 * i], d = pairs[2 * i + 1];
+        memmove((char *)k_pool + d * block_bytes, (char *)k_pool + s * block_bytes, block_bytes);
+        memmove((char *)v_pool + d * block_bytes, (char *)v_pool + s * block_bytes, block_bytes);
+    }
+}
+
+/* Swap-out gather: staging is [n][2][block_bytes] (K block then V block). */
+void orc_gather_blocks(void *staging, const void *k_pool, const void *v_pool,
+                       const int32_t *ids, int64_t n, int64_t block_bytes) {
+    for (int64_t i = 0; i < n; ++i) {
+        memcpy((char *)staging + (2 * i) * block_bytes, (const char *)k_pool + ids[i] * block_bytes,
+               block_bytes);
+        memcpy((char *)staging + (2 * i + 1) * block_bytes,
+               (const char *)v_pool + ids[i] * block_bytes, block_bytes);
+    }
+}
+
+/* Swap-in scatter: inverse of orc_gather_blocks. */
+void orc_scatter_blocks(void *k_pool, void *v_pool, const void *staging, const int32_t *ids,
+                        int64_t n, int64_t block_bytes) {
+    for (int64_t i = 0; i < n; ++i) {
+        memcpy((char *)k_pool + ids[i] * block_bytes, (const char *)staging + (2 * i) * block_bytes,
+               block_bytes);
+        memcpy((char *)v_pool + ids[i] * block_bytes,
+               (const char *)staging + (2 * i + 1) * block_bytes, block_bytes);
+    }
+}
+
+/* ------------------------------------------------------------------------ */
+/* Per-token KV quantization: src/forward/cpu.rs:667-711.                    */
+/* ------------------------------------------------------------------------ */
+
+/* quantize_i8 (:667-680): scale = max|x| / 127; q = round(x/scale) clamped. */
+float orc_quantize_i8(const float *x, int64_t n, int8_t *q) {
+    float mx = 0.0f;
+    for (int64_t i = 0; i < n; ++i) mx = fmaxf(mx, fabsf(x[i]));
+    float scale = mx / 127.0f;
+    if (!(scale > 0.0f)) {
+        memset(q, 0, n);
+        return 0.0f;
+    }
+    for (int64_t i = 0; i < n; ++i) {
+        float r = roundf(x[i] / scale);
+        q[i] = (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
+    }
+    return scale;
+}
+
+/* quantize_i4 (:685-700): scale = max|x| / 7; nibbles two per byte, element i
+ * in byte i/2, low nibble for even i. */
+float orc_quantize_i4(const float *x, int64_t n, uint8_t *packed) {
+    memset(packed, 0, (n + 1) / 2);
+    float mx = 0.0f;
+    for (int64_t i = 0; i < n; ++i) mx = fmaxf(mx, fabsf(x[i]));
+    float scale = mx / 7.0f;
+    if (!(scale > 0.0f)) return 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        int8_t q = (int8_t)fminf(fmaxf(roundf(x[i] / scale), -7.0f), 7.0f);
+        uint8_t nib = (uint8_t)q & 0x0f;
+        packed[i / 2] |= (i % 2 == 0) ? nib : (uint8_t)(nib << 4);
+    }
+    return scale;
+}
+
+/* read_i4 (:706-711). */
+float orc_read_i4(const uint8_t *packed, int64_t base, int64_t i) {
+    uint8_t byte = packed[base + i / 2];
+    uint8_t nib = (i % 2 == 0) ? (byte & 0x0f) : (byte >> 4);
+    int code = nib >= 8 ? (int)nib - 16 : (int)nib;
+    return (float)code;
+}

@@ -1,0 +1,80 @@
+"""libdlmk.so loads, exports exactly what include/dlmk.h declares, and rejects
+bad arguments before touching the GPU (no compute calls here)."""
+import ctypes as C
+import os
+import re
+
+import pytest
+
+from dlm_amd import _lib
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include",
+                      "dlmk.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(dlmk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_entry_points():
+    syms = declared_symbols()
+    for must in ("dlmk_kv_append", "dlmk_paged_decode_attention", "dlmk_copy_blocks",
+                 "dlmk_swap_out", "dlmk_swap_in", "dlmk_cache_append_tokens"):
+        assert must in syms
+
+
+def test_library_exports_every_declared_symbol(dlmk):
+    missing = [s for s in declared_symbols() if not hasattr(dlmk, s)]
+    assert not missing, missing
+
+
+def test_python_binding_covers_the_header():
+    assert sorted(_lib.SIGNATURES) == declared_symbols()
+
+
+def test_exported_symbols_are_c_linkage():
+    out = os.popen(f"nm -D --defined-only {_lib.LIB_PATH}").read()
+    exported = set(re.findall(r"\b(dlmk_[a-z0-9_]+)\b", out))
+    assert set(declared_symbols()) <= exported
+
+
+def test_abi_version(dlmk):
+    assert dlmk.dlmk_abi_version() == 1
+
+
+def test_argument_errors_before_any_launch(dlmk):
+    # Negative sizes and null pointers fail on the host with DLMK_ERR_INVALID_ARG.
+    rc = dlmk.dlmk_kv_append(None, None, None, None, None, None, -1, 8, 128, 16, 10, 1)
+    assert rc == _lib.DLMK_ERR_INVALID_ARG
+    assert "bad sizes" in _lib.last_error()
+    rc = dlmk.dlmk_kv_append(None, None, None, None, None, None, 4, 8, 128, 16, 10, 1)
+    assert rc == _lib.DLMK_ERR_INVALID_ARG
+    rc = dlmk.dlmk_kv_append(None, 1, 1, 1, 1, 1, 4, 8, 12, 16, 10, 1)  # 12*2 % 16 != 0
+    assert rc == _lib.DLMK_ERR_UNSUPPORTED
+    # Zero tokens is a successful no-op.
+    assert dlmk.dlmk_kv_append(None, None, None, None, None, None, 0, 8, 128, 16, 10, 1) == 0
+    rc = dlmk.dlmk_copy_blocks(None, 1, 1, 1, 3, 100, 10)  # block_bytes not multiple of 16
+    assert rc == _lib.DLMK_ERR_INVALID_ARG
+    rc = dlmk.dlmk_paged_decode_attention(None, 1, 1, 1, 1, 1, 1, 1, 1, 4, 1, 32, 6, 128, 16,
+                                          8, 100, 0.1, None, 0)  # 32 % 6 != 0
+    assert rc == _lib.DLMK_ERR_INVALID_ARG
+    rc = dlmk.dlmk_paged_decode_attention(None, 1, 1, 1, 1, 1, 1, 1, 1, 4, 1, 32, 8, 128, 32,
+                                          8, 100, 0.1, None, 0)  # block_size 32
+    assert rc == _lib.DLMK_ERR_UNSUPPORTED
+    rc = dlmk.dlmk_paged_decode_attention(None, 1, 1, 1, 1, 1, 1, 1, 1, 4, 1, 32, 8, 128, 16,
+                                          64, 100, 0.1, None, 0)  # needs workspace
+    assert rc == _lib.DLMK_ERR_WORKSPACE
+    rc = dlmk.dlmk_swap_out(None, 1, 1, 1, 1, 2, 64, 10, 1, 100)  # staging 100 < 256
+    assert rc == _lib.DLMK_ERR_WORKSPACE
+
+
+def test_workspace_size_formula(dlmk):
+    # One partition (<= 256 tokens) needs no workspace.
+    assert dlmk.dlmk_paged_attention_workspace_size(64, 1, 32, 128, 16, 16) == 0
+    # 4096-token tables: 16 partitions of (d + 2) floats per query row.
+    rows, parts = 64 * 32, 16
+    o = rows * parts * 128 * 4
+    assert dlmk.dlmk_paged_attention_workspace_size(64, 1, 32, 128, 16, 256) == \
+        (o + 255) // 256 * 256 + rows * parts * 8
