@@ -37,7 +37,24 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bound on the CPU baseline sample's work")
+    p.add_argument("--copy-calibration", action="store_true",
+                   help="only run dlmk_copy_blocks over 4096 64-KiB blocks (512 MiB read + "
+                        "512 MiB written per launch), to scale FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
+
+
+def copy_calibration(torch, ops, steps):
+    """A plain copy of known size: 4096 pairs of 64 KiB blocks per pool, K and V."""
+    dev = torch.device("cuda:0")
+    nb, bb = 8192, HKV * BS * D * 2
+    k = torch.zeros(nb * bb, dtype=torch.uint8, device=dev)
+    v = torch.zeros_like(k)
+    pairs = torch.stack([torch.arange(0, 4096), torch.arange(4096, 8192)], 1).int().to(dev)
+    for _ in range(steps):
+        ops.copy_blocks(k, v, pairs, bb)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration": {"launches": steps, "bytes_read_per_launch": 2 * 4096 * bb,
+                                           "bytes_written_per_launch": 2 * 4096 * bb}}))
 
 
 def attn_bytes(ctx, nq=1, out_bytes=2):
@@ -133,6 +150,9 @@ def main():
     import torch
     from dlm_amd import KvCacheConfig, PagedKvCache, ops
 
+    if args.copy_calibration:
+        copy_calibration(torch, ops, args.steps)
+        return
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev)
@@ -241,7 +261,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-            "kernel": "paged_attn_partition_kernel + paged_attn_combine_kernel (one launch pair)",
+            "kernel": "paged_attn_mfma_kernel + paged_attn_combine_kernel (one launch pair)",
         },
     }
     if not args.no_cpu_baseline:

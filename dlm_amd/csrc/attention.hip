@@ -6,26 +6,29 @@
 // softmax over the visible positions, out = sum p * v -- evaluated as a
 // streaming, HBM-bound pass over the paged pools.
 //
-// Work decomposition.  One work-group owns one (sequence, kv head, partition of
-// kPartition = 256 tokens) and serves every query row that reads that kv head:
-// the GQA group times the num_q_per_seq verify queries (ROWS rows).  K/V bytes
-// of a partition are therefore read from HBM exactly once.  Each wavefront owns
-// BPW consecutive 16-token blocks and issues all their K and V loads (16 bytes
-// per lane, each instruction one contiguous KiB of a tile) before doing any
-// maths, so a wave keeps BPW * 8 KiB (f16, d=128) in flight.
+// Work decomposition (both kernels).  One work-group owns one (sequence, kv
+// head, partition of P tokens) and serves every query row that reads that kv
+// head: the GQA group times the num_q_per_seq verify queries (ROWS rows).  K/V
+// bytes of a partition are therefore read from HBM exactly once.  Partition
+// blocks are dealt to the NW wavefronts round-robin.  Each wave computes an
+// exact softmax over its own tokens (max over all its scores first, so no
+// rescaling), the waves are merged in LDS, and partitions of one sequence are
+// merged by log-sum-exp in a second kernel (a sequence whose context fits one
+// partition is finished by the first).  Everything runs in the log2 domain
+// with log2(e) folded into the scale.
 //
-//   K tile [d/X][16][X]: load i of lane l is chunk row l/16 + 4i of token l%16,
-//     so one lane accumulates a 4-chunk partial dot for one token and the
-//     score needs only a 4-way cross-lane sum (xor 16, xor 32).
-//   V tile [d][16]: load i of lane l is X consecutive tokens of one dim, so a
-//     lane's accumulator is ROWS x (loads) floats and the final sum is across
-//     the 16/X lanes sharing a dim.
-//
-// Softmax is computed per wave over its own tokens (max, exp2, sum, all in
-// the log2 domain with log2(e) folded into the scale), the waves are merged in
-// LDS, and partitions of one sequence are merged by log-sum-exp in a second
-// kernel.  A sequence whose context fits one partition is finished by the
-// first kernel.
+// f16 / bf16 pools: matrix-core kernel.  Per 16-token block and wave:
+//   S^T (16 tokens x 16 rows) = K (16 x d) . Q^T (d x 16)
+//     v_mfma_f32_16x16x32_{f16,bf16}, d/32 steps.  A K-tile load of lane l
+//     (chunk row l/16 + 4i of token l%16, 16 bytes) is exactly the A operand,
+//     the query rows (zero-padded to 16) are the B operand.  The accumulator
+//     lands as lane l = (row l%16, tokens 4(l/16)..+3).
+//   O (16 rows x d) += P (16 x 16 tokens) . V (16 tokens x d)
+//     v_mfma_f32_16x16x16_{f16,bf16}, d/16 steps.  S^T's accumulator layout
+//     IS the A-operand layout of this product, so P never leaves registers;
+//     the B operand is 4 tokens x 1 dim = 8 contiguous bytes of the V tile
+//     [d][16].
+// f32 pools: VALU kernel (dot products with FMA, cross-lane sums).
 
 #include <hip/hip_runtime.h>
 
@@ -36,67 +39,16 @@
 
 namespace {
 
-constexpr int kBlock = 16;        // tokens per KV block (dlm: src/main.rs:455)
-constexpr int kPartition = 256;   // tokens per work-group
+constexpr int kBlock = 16;          // tokens per KV block (dlm: src/main.rs:455)
+constexpr int kMinPartition = 256;  // smallest partition of any kernel (sizes the workspace)
 constexpr float kLog2e = 1.4426950408889634f;
 
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
-
-template <typename T>
-struct Elem;
-template <>
-struct Elem<float> {
-    static constexpr int X = 4;
-};
-template <>
-struct Elem<_Float16> {
-    static constexpr int X = 8;
-};
-
-// acc + dot of two 16-byte chunks.
-template <typename T>
-__device__ __forceinline__ float dot_chunk(const uint4 &a, const uint4 &b, float acc);
-
-template <>
-__device__ __forceinline__ float dot_chunk<float>(const uint4 &a, const uint4 &b, float acc) {
-    acc = fmaf(__uint_as_float(a.x), __uint_as_float(b.x), acc);
-    acc = fmaf(__uint_as_float(a.y), __uint_as_float(b.y), acc);
-    acc = fmaf(__uint_as_float(a.z), __uint_as_float(b.z), acc);
-    acc = fmaf(__uint_as_float(a.w), __uint_as_float(b.w), acc);
-    return acc;
-}
-
-template <>
-__device__ __forceinline__ float dot_chunk<_Float16>(const uint4 &a, const uint4 &b, float acc) {
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.x), __builtin_bit_cast(f16x2, b.x), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.y), __builtin_bit_cast(f16x2, b.y), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.z), __builtin_bit_cast(f16x2, b.z), acc, false);
-    acc = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, a.w), __builtin_bit_cast(f16x2, b.w), acc, false);
-    return acc;
-}
-
-// Widen one 16-byte chunk to X floats (exact).
-template <typename T>
-__device__ __forceinline__ void widen(const uint4 &c, float *out);
-
-template <>
-__device__ __forceinline__ void widen<float>(const uint4 &c, float *out) {
-    out[0] = __uint_as_float(c.x);
-    out[1] = __uint_as_float(c.y);
-    out[2] = __uint_as_float(c.z);
-    out[3] = __uint_as_float(c.w);
-}
-
-template <>
-__device__ __forceinline__ void widen<_Float16>(const uint4 &c, float *out) {
-    const uint32_t w[4] = {c.x, c.y, c.z, c.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        f16x2 h = __builtin_bit_cast(f16x2, w[i]);
-        out[2 * i] = (float)h[0];
-        out[2 * i + 1] = (float)h[1];
-    }
-}
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ void store_out(void *out, int out_dtype, int64_t idx, float v) {
     if (out_dtype == DLMK_F32) {
@@ -104,12 +56,7 @@ __device__ __forceinline__ void store_out(void *out, int out_dtype, int64_t idx,
     } else if (out_dtype == DLMK_F16) {
         static_cast<_Float16 *>(out)[idx] = (_Float16)v;
     } else {
-        // bf16, round to nearest even (NaN kept quiet).
-        uint32_t u = __float_as_uint(v);
-        uint16_t r = (u & 0x7fffffffu) > 0x7f800000u
-                         ? (uint16_t)((u >> 16) | 0x40)
-                         : (uint16_t)((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
-        static_cast<uint16_t *>(out)[idx] = r;
+        static_cast<__bf16 *>(out)[idx] = (__bf16)v;  // round to nearest even
     }
 }
 
@@ -127,43 +74,248 @@ __device__ __forceinline__ float xor_max(float v) {
     return v;
 }
 
+__device__ __forceinline__ int parts_of(int ctx, int P) { return ctx > P ? (ctx + P - 1) / P : 1; }
+
+// Shared epilogue: merge the NW waves' (m, l, O) of one work-group and either
+// finish the rows (single-partition sequence) or store the partition partial.
+template <int ROWS, int D, int NW, int GQA, int NQ>
+__device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][D],
+                                            const float (&ml_lds)[NW][ROWS][2], void *out,
+                                            int out_dtype, int seq, int kvh, int part,
+                                            int nparts, int num_q_heads, int max_parts,
+                                            float *ws_o, float *ws_ml) {
+    for (int idx = threadIdx.x; idx < ROWS * D; idx += NW * 64) {
+        const int r = idx / D, d = idx - r * D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, ml_lds[w][r][0]);
+        float O = 0.f, L = 0.f;
+        if (M != -INFINITY) {
+#pragma unroll
+            for (int w = 0; w < NW; ++w) {
+                const float mw = ml_lds[w][r][0];
+                const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
+                L = fmaf(f, ml_lds[w][r][1], L);
+                O = fmaf(f, o_lds[w][r][d], O);
+            }
+        }
+        const int j = r / GQA, h = kvh * GQA + r % GQA;
+        const int64_t row = (int64_t)(seq * NQ + j) * num_q_heads + h;
+        if (nparts == 1) {
+            store_out(out, out_dtype, row * D + d, L > 0.f ? O / L : 0.f);
+        } else {
+            const int64_t slot = row * max_parts + part;
+            ws_o[slot * D + d] = O;
+            if (d == 0) {
+                ws_ml[2 * slot] = M;
+                ws_ml[2 * slot + 1] = L;
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------------------
-// Pass 1: one work-group per (partition, kv head, sequence).
+// Matrix-core partition kernel (f16 / bf16 pools).
 // ---------------------------------------------------------------------------
-template <typename T, int D, int GQA, int NQ, int NWAVES>
-__global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<_Float16> {
+    using x8 = f16x8;
+    using x4 = f16x4;
+    static __device__ __forceinline__ f32x4 qk(x8 a, x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 pv(x4 a, x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mfma<__bf16> {
+    using x8 = bf16x8;
+    using x4 = bf16x4;
+    static __device__ __forceinline__ f32x4 qk(x8 a, x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 pv(x4 a, x4 b, f32x4 c) {
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                         __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+    }
+};
+
+template <typename T, int D, int GQA, int NQ, int NW, int NB>
+__global__ __launch_bounds__(NW * 64) void paged_attn_mfma_kernel(
     void *__restrict__ out, int out_dtype, const T *__restrict__ q,
     const T *__restrict__ k_pool, const T *__restrict__ v_pool,
     const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
     int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
     int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
-    constexpr int X = Elem<T>::X;          // elements per 16-byte chunk
-    constexpr int CPL = D / X;             // chunks per token row
-    constexpr int KI = CPL / 4;            // 16-byte loads per lane per block (K and V alike)
-    constexpr int CPD = kBlock / X;        // V chunks per dim row of a tile
+    using M = Mfma<T>;
+    using x8 = typename M::x8;
+    using x4 = typename M::x4;
     constexpr int ROWS = GQA * NQ;
-    constexpr int BPW = kPartition / kBlock / NWAVES;  // blocks per wave
-    constexpr int TILE = D * kBlock;       // elements per (block, kv head) tile
-    static_assert(CPL % 4 == 0 && BPW >= 1, "unsupported geometry");
+    constexpr int KI = D / 32;           // QK steps = 16-byte K loads per lane per block
+    constexpr int VN = D / 16;           // PV steps = 8-byte V loads per lane per block
+    constexpr int P = NW * NB * kBlock;  // tokens per work-group
+    constexpr int TILE = D * kBlock;     // elements per (block, kv head) tile
+    static_assert(ROWS <= 16 && D % 32 == 0, "unsupported geometry");
 
-    __shared__ float p_lds[NWAVES][BPW][ROWS][kBlock];
-    __shared__ float o_lds[NWAVES][ROWS][D];
-    __shared__ float ml_lds[NWAVES][ROWS][2];
+    __shared__ float o_lds[NW][ROWS][D];
+    __shared__ float ml_lds[NW][ROWS][2];
 
     const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
     // A length beyond the table width is clamped: no read past a table row and
     // no partition index past max_parts.
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
-    const int nparts = ctx > kPartition ? (ctx + kPartition - 1) / kPartition : 1;
+    const int nparts = parts_of(ctx, P);
+    if (part >= nparts) return;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n = lane & 15;  // lane group, row (QK) / dim (PV) index
+    const int nblk_seq = (ctx + kBlock - 1) / kBlock;
+    const int32_t *table = block_tables + (int64_t)seq * max_blocks;
+
+    // Q^T operand: row n of the group, dims 32i + 8g .. +7 (zero beyond ROWS).
+    x8 qb[KI];
+    {
+        const int j = n / GQA, h = kvh * GQA + n % GQA;
+        const x8 *qp = reinterpret_cast<const x8 *>(q + ((int64_t)(seq * NQ + j) * num_q_heads + h) * D);
+#pragma unroll
+        for (int i = 0; i < KI; ++i) qb[i] = n < ROWS ? qp[g + 4 * i] : x8{};
+    }
+    // Causal limit of this lane's row (verify query n / GQA).
+    const int limit = n < ROWS ? ctx - NQ + n / GQA + 1 : ctx;
+
+    // This wave's blocks: partition block b*NW + wave.
+    int lbs[NB];
+    int64_t blk[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int lb = part * (NW * NB) + b * NW + wave;
+        const int64_t id = lb < nblk_seq ? (int64_t)table[lb] : -1;
+        lbs[b] = lb;
+        blk[b] = (id >= 0 && id < num_blocks) ? id : -1;
+    }
+
+    // Scores S^T: s[b][j] = row n, token 4g + j of block b.
+    float s[NB][4];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+        if (blk[b] >= 0) {
+            const x8 *kp = reinterpret_cast<const x8 *>(k_pool + (blk[b] * num_kv_heads + kvh) * TILE);
+#pragma unroll
+            for (int i = 0; i < KI; ++i) c = M::qk(kp[64 * i + lane], qb[i], c);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int pos = lbs[b] * kBlock + 4 * g + j;
+            s[b][j] = (blk[b] >= 0 && pos < limit) ? c[j] * scale_log2 : -INFINITY;
+        }
+    }
+
+    // Exact per-wave row max: own scores, then the 4 lane groups.
+    float m = -INFINITY;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) m = fmaxf(m, s[b][j]);
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+
+    // O += P . V; P rounded to the operand type, and l sums the rounded P.
+    f32x4 acc[VN];
+#pragma unroll
+    for (int k = 0; k < VN; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float lsum = 0.f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        if (blk[b] < 0) continue;
+        x4 pa;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const T ph = (T)(m == -INFINITY ? 0.f : exp2f(s[b][j] - m));
+            pa[j] = ph;
+            lsum += (float)ph;
+        }
+        const T *vt = v_pool + (blk[b] * num_kv_heads + kvh) * TILE;
+        // Tokens past the context in the last block hold stale bytes (maybe
+        // NaN); zero them so p = 0 contributes exactly nothing.
+        const int valid = ctx - lbs[b] * kBlock;
+#pragma unroll
+        for (int k = 0; k < VN; ++k) {
+            x4 vv = *reinterpret_cast<const x4 *>(vt + (16 * k + n) * kBlock + 4 * g);
+            if (valid < kBlock) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * g + e >= valid) vv[e] = T(0.f);
+            }
+            acc[k] = M::pv(pa, vv, acc[k]);
+        }
+    }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+
+    // acc[k][j] = O[row 4g + j][dim 16k + n].
+#pragma unroll
+    for (int k = 0; k < VN; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (4 * g + j < ROWS) o_lds[wave][4 * g + j][16 * k + n] = acc[k][j];
+    if (g == 0 && n < ROWS) {
+        ml_lds[wave][n][0] = m;
+        ml_lds[wave][n][1] = lsum;
+    }
+    __syncthreads();
+    merge_waves<ROWS, D, NW, GQA, NQ>(o_lds, ml_lds, out, out_dtype, seq, kvh, part, nparts,
+                                      num_q_heads, max_parts, ws_o, ws_ml);
+}
+
+// ---------------------------------------------------------------------------
+// VALU partition kernel (f32 pools).
+//   K tile [d/4][16][4]: load i of lane l is chunk row l/16 + 4i of token l%16,
+//     so one lane holds a 4-chunk partial dot for one token and the score
+//     needs a 4-way cross-lane sum (xor 16, xor 32).
+//   V tile [d][16]: load i of lane l is 4 consecutive tokens of one dim, so a
+//     lane's accumulator is ROWS x (loads) floats summed across the 4 lanes
+//     sharing a dim.
+// ---------------------------------------------------------------------------
+template <int D, int GQA, int NQ, int NW>
+__global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
+    void *__restrict__ out, int out_dtype, const float *__restrict__ q,
+    const float *__restrict__ k_pool, const float *__restrict__ v_pool,
+    const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
+    int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
+    int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
+    constexpr int X = 4;                    // floats per 16-byte chunk
+    constexpr int CPL = D / X;              // chunks per token row
+    constexpr int KI = CPL / 4;             // 16-byte loads per lane per block (K and V alike)
+    constexpr int CPD = kBlock / X;         // V chunks per dim row of a tile
+    constexpr int ROWS = GQA * NQ;
+    constexpr int P = kMinPartition;
+    constexpr int BPW = P / kBlock / NW;    // blocks per wave
+    constexpr int TILE = D * kBlock;
+    static_assert(CPL % 4 == 0 && BPW >= 1, "unsupported geometry");
+
+    __shared__ float p_lds[NW][BPW][ROWS][kBlock];
+    __shared__ float o_lds[NW][ROWS][D];
+    __shared__ float ml_lds[NW][ROWS][2];
+
+    const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    const int nparts = parts_of(ctx, P);
     if (part >= nparts) return;
 
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nblk_seq = (ctx + kBlock - 1) / kBlock;
-    const int first_lb = part * (kPartition / kBlock) + wave * BPW;
+    const int first_lb = part * (P / kBlock) + wave * BPW;
     const int32_t *table = block_tables + (int64_t)seq * max_blocks;
 
-    // Physical ids of this wave's blocks (wave-uniform).
     int64_t blk[BPW];
 #pragma unroll
     for (int b = 0; b < BPW; ++b) {
@@ -172,7 +324,6 @@ __global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
         blk[b] = (id >= 0 && id < num_blocks) ? id : -1;
     }
 
-    // Issue every K and V load of the wave up front.
     uint4 kb[BPW][KI], vb[BPW][KI];
 #pragma unroll
     for (int b = 0; b < BPW; ++b) {
@@ -190,7 +341,6 @@ __global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
         }
     }
 
-    // Query chunks matching this lane's K chunks.
     uint4 qr[ROWS][KI];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
@@ -201,7 +351,6 @@ __global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
         for (int i = 0; i < KI; ++i) qr[r][i] = qp[(lane >> 4) + 4 * i];
     }
 
-    // Scores for token lane%16 of each block; log2 domain.
     const int tok = lane & 15;
     float s[BPW][ROWS];
 #pragma unroll
@@ -210,7 +359,12 @@ __global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
         for (int r = 0; r < ROWS; ++r) {
             float acc = 0.f;
 #pragma unroll
-            for (int i = 0; i < KI; ++i) acc = dot_chunk<T>(qr[r][i], kb[b][i], acc);
+            for (int i = 0; i < KI; ++i) {
+                acc = fmaf(__uint_as_float(qr[r][i].x), __uint_as_float(kb[b][i].x), acc);
+                acc = fmaf(__uint_as_float(qr[r][i].y), __uint_as_float(kb[b][i].y), acc);
+                acc = fmaf(__uint_as_float(qr[r][i].z), __uint_as_float(kb[b][i].z), acc);
+                acc = fmaf(__uint_as_float(qr[r][i].w), __uint_as_float(kb[b][i].w), acc);
+            }
             acc += __shfl_xor(acc, 16);
             acc += __shfl_xor(acc, 32);
             s[b][r] = acc;
@@ -219,7 +373,7 @@ __global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
     float m[ROWS], l[ROWS];
 #pragma unroll
     for (int r = 0; r < ROWS; ++r) {
-        const int limit = ctx - NQ + r / GQA + 1;  // causal limit of verify query r/GQA
+        const int limit = ctx - NQ + r / GQA + 1;
         float mx = -INFINITY;
 #pragma unroll
         for (int b = 0; b < BPW; ++b) {
@@ -240,7 +394,6 @@ __global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
         l[r] = xor_sum<16>(sum);
     }
 
-    // Probabilities to LDS: lane group g (= lane/16) writes rows r with r%4 == g.
 #pragma unroll
     for (int b = 0; b < BPW; ++b)
 #pragma unroll
@@ -248,7 +401,6 @@ __global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
             if ((r & 3) == (lane >> 4)) p_lds[wave][b][r][tok] = s[b][r];
     __syncthreads();
 
-    // acc[r][i] covers dim (64 i + lane) / CPD over tokens tg*X .. tg*X+X-1.
     const int tg = lane % CPD;
     float acc[ROWS][KI];
 #pragma unroll
@@ -264,13 +416,11 @@ __global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
         for (int r = 0; r < ROWS; ++r)
 #pragma unroll
             for (int e = 0; e < X; ++e) pr[r][e] = p_lds[wave][b][r][tg * X + e];
-        // Tokens past the context in the last block hold stale bytes (maybe
-        // NaN); zero them so p = 0 contributes exactly nothing.
         const int valid = ctx - (first_lb + b) * kBlock;
 #pragma unroll
         for (int i = 0; i < KI; ++i) {
-            float v[X];
-            widen<T>(vb[b][i], v);
+            float v[X] = {__uint_as_float(vb[b][i].x), __uint_as_float(vb[b][i].y),
+                          __uint_as_float(vb[b][i].z), __uint_as_float(vb[b][i].w)};
             if (valid < kBlock) {
 #pragma unroll
                 for (int e = 0; e < X; ++e)
@@ -302,36 +452,8 @@ __global__ __launch_bounds__(NWAVES * 64) void paged_attn_partition_kernel(
         }
     }
     __syncthreads();
-
-    // Merge the waves; finish or write the partition's partial.
-    for (int idx = threadIdx.x; idx < ROWS * D; idx += NWAVES * 64) {
-        const int r = idx / D, d = idx - r * D;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < NWAVES; ++w) M = fmaxf(M, ml_lds[w][r][0]);
-        float O = 0.f, L = 0.f;
-        if (M != -INFINITY) {
-#pragma unroll
-            for (int w = 0; w < NWAVES; ++w) {
-                const float mw = ml_lds[w][r][0];
-                const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
-                L = fmaf(f, ml_lds[w][r][1], L);
-                O = fmaf(f, o_lds[w][r][d], O);
-            }
-        }
-        const int j = r / GQA, h = kvh * GQA + r % GQA;
-        const int64_t row = (int64_t)(seq * NQ + j) * num_q_heads + h;
-        if (nparts == 1) {
-            store_out(out, out_dtype, row * D + d, L > 0.f ? O / L : 0.f);
-        } else {
-            const int64_t slot = row * max_parts + part;
-            ws_o[slot * D + d] = O;
-            if (d == 0) {
-                ws_ml[2 * slot] = M;
-                ws_ml[2 * slot + 1] = L;
-            }
-        }
-    }
+    merge_waves<ROWS, D, NW, GQA, NQ>(o_lds, ml_lds, out, out_dtype, seq, kvh, part, nparts,
+                                      num_q_heads, max_parts, ws_o, ws_ml);
 }
 
 // ---------------------------------------------------------------------------
@@ -341,11 +463,11 @@ template <int D>
 __global__ __launch_bounds__(64) void paged_attn_combine_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
     const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
-    int max_parts) {
+    int max_blocks, int partition, int max_parts) {
     constexpr int DPL = D / 64;  // dims per lane
     const int seq = blockIdx.y;
-    const int ctx = min(ctx_lens[seq], max_parts * kPartition);
-    const int nparts = ctx > kPartition ? (ctx + kPartition - 1) / kPartition : 1;
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    const int nparts = parts_of(ctx, partition);
     if (nparts == 1) return;
     const int lane = threadIdx.x;
     const int64_t row = (int64_t)seq * rows_per_seq + blockIdx.x;
@@ -384,66 +506,102 @@ struct Args {
     int B, NQ, Hq, Hkv, max_blocks;
     int64_t num_blocks;
     float scale;
-    float *ws_o, *ws_ml;
-    int max_parts;
+    void *workspace;
+    int64_t ws_o_bytes;
     hipStream_t stream;
 };
 
-template <typename T, int D, int GQA, int NQ>
-int launch(const Args &a) {
-    constexpr int ROWS = GQA * NQ;
-    constexpr int NWAVES = ROWS <= 4 ? 4 : 8;
-    dim3 grid((unsigned)a.max_parts, (unsigned)a.Hkv, (unsigned)a.B);
-    hipLaunchKernelGGL((paged_attn_partition_kernel<T, D, GQA, NQ, NWAVES>), grid,
-                       dim3(NWAVES * 64), 0, a.stream, a.out, a.out_dtype,
+int64_t parts_for(int max_blocks, int partition) {
+    int64_t tokens = (int64_t)max_blocks * kBlock;
+    return tokens > partition ? dlmk::ceil_div(tokens, partition) : 1;
+}
+
+template <typename T>
+using PartitionKernel = void (*)(void *, int, const T *, const T *, const T *, const int32_t *,
+                                 const int32_t *, int, int, int, int64_t, float, int, float *,
+                                 float *);
+
+template <typename T, int D>
+int launch_pair(const Args &a, PartitionKernel<T> kernel, int nw, int partition) {
+    const int max_parts = (int)parts_for(a.max_blocks, partition);
+    float *ws_o = nullptr, *ws_ml = nullptr;
+    if (max_parts > 1) {
+        ws_o = static_cast<float *>(a.workspace);
+        ws_ml = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + a.ws_o_bytes);
+    }
+    dim3 grid((unsigned)max_parts, (unsigned)a.Hkv, (unsigned)a.B);
+    hipLaunchKernelGGL(kernel, grid, dim3(nw * 64), 0, a.stream, a.out, a.out_dtype,
                        static_cast<const T *>(a.q), static_cast<const T *>(a.k_pool),
                        static_cast<const T *>(a.v_pool), a.tables, a.ctx_lens, a.Hq, a.Hkv,
-                       a.max_blocks, a.num_blocks, a.scale * kLog2e, a.max_parts, a.ws_o,
-                       a.ws_ml);
-    if (a.max_parts > 1)
+                       a.max_blocks, a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
+    if (max_parts > 1)
         hipLaunchKernelGGL(paged_attn_combine_kernel<D>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
-                           dim3(64), 0, a.stream, a.out, a.out_dtype, a.ws_o, a.ws_ml,
-                           a.ctx_lens, a.NQ * a.Hq, a.max_parts);
+                           dim3(64), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
+                           a.NQ * a.Hq, a.max_blocks, partition, max_parts);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return dlmk::fail((int)e, "dlmk_paged_decode_attention launch: %s", hipGetErrorString(e));
     return DLMK_OK;
 }
 
+// Matrix-core path: 4 waves x 8 blocks = 512-token partitions.
+template <typename T, int D, int GQA, int NQ>
+int launch_mfma(const Args &a) {
+    constexpr int NW = 4, NB = 8;
+    return launch_pair<T, D>(a, &paged_attn_mfma_kernel<T, D, GQA, NQ, NW, NB>, NW,
+                             NW * NB * kBlock);
+}
+
+template <int D, int GQA, int NQ>
+int launch_valu(const Args &a) {
+    constexpr int NW = GQA * NQ <= 4 ? 4 : 8;
+    return launch_pair<float, D>(a, &paged_attn_valu_kernel<D, GQA, NQ, NW>, NW, kMinPartition);
+}
+
+int unsupported_rows(int gqa, int nq) {
+    return dlmk::fail(DLMK_ERR_UNSUPPORTED,
+                      "dlmk_paged_decode_attention: no kernel for GQA group %d x %d queries", gqa, nq);
+}
+
 template <typename T, int D>
-int dispatch_rows(const Args &a, int gqa) {
+int dispatch_mfma(const Args &a, int gqa) {
     switch (gqa * 16 + a.NQ) {
-        case 1 * 16 + 1: return launch<T, D, 1, 1>(a);
-        case 1 * 16 + 2: return launch<T, D, 1, 2>(a);
-        case 1 * 16 + 4: return launch<T, D, 1, 4>(a);
-        case 2 * 16 + 1: return launch<T, D, 2, 1>(a);
-        case 2 * 16 + 2: return launch<T, D, 2, 2>(a);
-        case 2 * 16 + 4: return launch<T, D, 2, 4>(a);
-        case 4 * 16 + 1: return launch<T, D, 4, 1>(a);
-        case 4 * 16 + 2: return launch<T, D, 4, 2>(a);
-        case 8 * 16 + 1: return launch<T, D, 8, 1>(a);
-        default:
-            return dlmk::fail(DLMK_ERR_UNSUPPORTED,
-                              "dlmk_paged_decode_attention: no kernel for GQA group %d x %d queries",
-                              gqa, a.NQ);
+        case 1 * 16 + 1: return launch_mfma<T, D, 1, 1>(a);
+        case 1 * 16 + 2: return launch_mfma<T, D, 1, 2>(a);
+        case 1 * 16 + 4: return launch_mfma<T, D, 1, 4>(a);
+        case 2 * 16 + 1: return launch_mfma<T, D, 2, 1>(a);
+        case 2 * 16 + 2: return launch_mfma<T, D, 2, 2>(a);
+        case 2 * 16 + 4: return launch_mfma<T, D, 2, 4>(a);
+        case 4 * 16 + 1: return launch_mfma<T, D, 4, 1>(a);
+        case 4 * 16 + 2: return launch_mfma<T, D, 4, 2>(a);
+        case 4 * 16 + 4: return launch_mfma<T, D, 4, 4>(a);
+        case 8 * 16 + 1: return launch_mfma<T, D, 8, 1>(a);
+        case 8 * 16 + 2: return launch_mfma<T, D, 8, 2>(a);
+        case 16 * 16 + 1: return launch_mfma<T, D, 16, 1>(a);
+        default: return unsupported_rows(gqa, a.NQ);
     }
 }
 
-template <typename T>
-int dispatch_dim(const Args &a, int head_dim, int gqa) {
-    switch (head_dim) {
-        case 64: return dispatch_rows<T, 64>(a, gqa);
-        case 128: return dispatch_rows<T, 128>(a, gqa);
-        default:
-            return dlmk::fail(DLMK_ERR_UNSUPPORTED,
-                              "dlmk_paged_decode_attention: head_dim %d unsupported (64, 128)",
-                              head_dim);
+template <int D>
+int dispatch_valu(const Args &a, int gqa) {
+    switch (gqa * 16 + a.NQ) {
+        case 1 * 16 + 1: return launch_valu<D, 1, 1>(a);
+        case 1 * 16 + 2: return launch_valu<D, 1, 2>(a);
+        case 1 * 16 + 4: return launch_valu<D, 1, 4>(a);
+        case 2 * 16 + 1: return launch_valu<D, 2, 1>(a);
+        case 2 * 16 + 2: return launch_valu<D, 2, 2>(a);
+        case 2 * 16 + 4: return launch_valu<D, 2, 4>(a);
+        case 4 * 16 + 1: return launch_valu<D, 4, 1>(a);
+        case 4 * 16 + 2: return launch_valu<D, 4, 2>(a);
+        case 8 * 16 + 1: return launch_valu<D, 8, 1>(a);
+        default: return unsupported_rows(gqa, a.NQ);
     }
 }
 
-int64_t parts_for(int max_blocks) {
-    int64_t tokens = (int64_t)max_blocks * kBlock;
-    return tokens > kPartition ? dlmk::ceil_div(tokens, kPartition) : 1;
+int bad_dim(int head_dim, const char *dims) {
+    return dlmk::fail(DLMK_ERR_UNSUPPORTED,
+                      "dlmk_paged_decode_attention: head_dim %d unsupported for this dtype (%s)",
+                      head_dim, dims);
 }
 
 }  // namespace
@@ -456,7 +614,7 @@ size_t dlmk_paged_attention_workspace_size(int num_seqs, int num_q_per_seq, int 
     if (num_seqs <= 0 || num_q_per_seq <= 0 || num_q_heads <= 0 || head_dim <= 0 ||
         max_blocks_per_seq <= 0)
         return 0;
-    const int64_t parts = parts_for(max_blocks_per_seq);
+    const int64_t parts = parts_for(max_blocks_per_seq, kMinPartition);
     if (parts <= 1) return 0;
     const int64_t rows = (int64_t)num_seqs * num_q_per_seq * num_q_heads;
     const int64_t o_bytes = rows * parts * head_dim * 4;
@@ -506,10 +664,10 @@ int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const vo
     a.num_blocks = num_blocks;
     a.scale = scale;
     a.stream = (hipStream_t)stream;
-    a.max_parts = (int)parts_for(max_blocks_per_seq);
-    a.ws_o = nullptr;
-    a.ws_ml = nullptr;
-    if (a.max_parts > 1) {
+    a.workspace = nullptr;
+    a.ws_o_bytes = 0;
+    const int64_t parts = parts_for(max_blocks_per_seq, kMinPartition);
+    if (parts > 1) {
         const size_t need = dlmk_paged_attention_workspace_size(
             num_seqs, num_q_per_seq, num_q_heads, head_dim, block_size, max_blocks_per_seq);
         if (!workspace || workspace_bytes < need)
@@ -520,18 +678,34 @@ int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const vo
             return dlmk::fail(DLMK_ERR_INVALID_ARG,
                               "dlmk_paged_decode_attention: workspace not 256-byte aligned");
         const int64_t rows = (int64_t)num_seqs * num_q_per_seq * num_q_heads;
-        const int64_t o_bytes = rows * a.max_parts * head_dim * 4;
-        a.ws_o = static_cast<float *>(workspace);
-        a.ws_ml = reinterpret_cast<float *>(static_cast<char *>(workspace) +
-                                            (o_bytes + 255) / 256 * 256);
+        a.workspace = workspace;
+        a.ws_o_bytes = (rows * parts * head_dim * 4 + 255) / 256 * 256;
     }
     const int gqa = num_q_heads / num_kv_heads;
     switch (dtype) {
-        case DLMK_F32: return dispatch_dim<float>(a, head_dim, gqa);
-        case DLMK_F16: return dispatch_dim<_Float16>(a, head_dim, gqa);
+        case DLMK_F32:
+            switch (head_dim) {
+                case 64: return dispatch_valu<64>(a, gqa);
+                case 128: return dispatch_valu<128>(a, gqa);
+                default: return bad_dim(head_dim, "64, 128");
+            }
+        case DLMK_F16:
+            switch (head_dim) {
+                case 64: return dispatch_mfma<_Float16, 64>(a, gqa);
+                case 128: return dispatch_mfma<_Float16, 128>(a, gqa);
+                case 256: return dispatch_mfma<_Float16, 256>(a, gqa);
+                default: return bad_dim(head_dim, "64, 128, 256");
+            }
+        case DLMK_BF16:
+            switch (head_dim) {
+                case 64: return dispatch_mfma<__bf16, 64>(a, gqa);
+                case 128: return dispatch_mfma<__bf16, 128>(a, gqa);
+                case 256: return dispatch_mfma<__bf16, 256>(a, gqa);
+                default: return bad_dim(head_dim, "64, 128, 256");
+            }
         default:
-            return dlmk::fail(DLMK_ERR_UNSUPPORTED,
-                              "dlmk_paged_decode_attention: KV dtype %d unsupported (f32, f16)", dtype);
+            return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_paged_decode_attention: bad KV dtype %d",
+                              dtype);
     }
 }
 
