@@ -10,7 +10,8 @@ import os
 import threading
 
 PKG = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(PKG, "libdlmk.so")
+# DLMK_LIBRARY points at another build of the same ABI (e.g. a tuning variant).
+LIB_PATH = os.environ.get("DLMK_LIBRARY") or os.path.join(PKG, "libdlmk.so")
 
 DLMK_F32, DLMK_F16, DLMK_BF16 = 0, 1, 2
 DLMK_OK = 0

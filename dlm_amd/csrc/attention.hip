@@ -43,6 +43,35 @@ constexpr int kBlock = 16;          // tokens per KV block (dlm: src/main.rs:455
 constexpr int kMinPartition = 256;  // smallest partition of any kernel (sizes the workspace)
 constexpr float kLog2e = 1.4426950408889634f;
 
+// Matrix-core kernel shape: waves per work-group, blocks per wave, prefetch
+// depth in tile loads (overridable at build time for tuning sweeps).
+#ifndef DLMK_MFMA_NW
+#define DLMK_MFMA_NW 4
+#endif
+#ifndef DLMK_MFMA_NB
+#define DLMK_MFMA_NB 8
+#endif
+#ifndef DLMK_MFMA_PD
+#define DLMK_MFMA_PD 2
+#endif
+// Minimum waves per SIMD the register allocation must allow (0: compiler's choice).
+#ifndef DLMK_MFMA_WPE
+#define DLMK_MFMA_WPE 0
+#endif
+// 1: stream K/V tiles with non-temporal loads (no reuse, keep them out of L2/MALL).
+#ifndef DLMK_MFMA_NT
+#define DLMK_MFMA_NT 1
+#endif
+
+template <typename V>
+__device__ __forceinline__ V stream_load(const V *p) {
+#if DLMK_MFMA_NT
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
+
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -146,8 +175,14 @@ struct Mfma<__bf16> {
     }
 };
 
-template <typename T, int D, int GQA, int NQ, int NW, int NB>
-__global__ __launch_bounds__(NW * 64) void paged_attn_mfma_kernel(
+#if DLMK_MFMA_WPE
+#define DLMK_MFMA_ATTRS __attribute__((amdgpu_waves_per_eu(DLMK_MFMA_WPE)))
+#else
+#define DLMK_MFMA_ATTRS
+#endif
+
+template <typename T, int D, int GQA, int NQ, int NW, int NB, int PD>
+__global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kernel(
     void *__restrict__ out, int out_dtype, const T *__restrict__ q,
     const T *__restrict__ k_pool, const T *__restrict__ v_pool,
     const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
@@ -166,7 +201,12 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_mfma_kernel(
     __shared__ float o_lds[NW][ROWS][D];
     __shared__ float ml_lds[NW][ROWS][2];
 
-    const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    // blockIdx.x = seq * num_kv_heads + kv head, blockIdx.y = partition: the
+    // dispatcher deals consecutive work-groups to the 8 XCDs round-robin, so
+    // with the (sequence, head) pair fastest every XCD gets the same mix of
+    // full and ragged partitions (partition-fastest would pin each XCD to one
+    // partition index, and late partitions exist only for long contexts).
+    const int part = blockIdx.y, kvh = blockIdx.x % num_kv_heads, seq = blockIdx.x / num_kv_heads;
     // A length beyond the table width is clamped: no read past a table row and
     // no partition index past max_parts.
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
@@ -190,71 +230,109 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_mfma_kernel(
     // Causal limit of this lane's row (verify query n / GQA).
     const int limit = n < ROWS ? ctx - NQ + n / GQA + 1 : ctx;
 
-    // This wave's blocks: partition block b*NW + wave.
+    // This wave's blocks: partition block b*NW + wave.  Blocks past the
+    // context (or with an id outside the pool) are masked, and their loads are
+    // pointed at the wave's first block so that every load can be issued
+    // unconditionally (a re-read hits L1/L2, not HBM): the loops below have no
+    // branches and the compiler can keep many loads in flight.
     int lbs[NB];
     int64_t blk[NB];
+    bool ok[NB];
+    int nvalid = 0;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int lb = part * (NW * NB) + b * NW + wave;
         const int64_t id = lb < nblk_seq ? (int64_t)table[lb] : -1;
         lbs[b] = lb;
-        blk[b] = (id >= 0 && id < num_blocks) ? id : -1;
+        ok[b] = id >= 0 && id < num_blocks;
+        blk[b] = id;
+        nvalid += ok[b];
     }
 
-    // Scores S^T: s[b][j] = row n, token 4g + j of block b.
-    float s[NB][4];
-#pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        f32x4 c = {0.f, 0.f, 0.f, 0.f};
-        if (blk[b] >= 0) {
-            const x8 *kp = reinterpret_cast<const x8 *>(k_pool + (blk[b] * num_kv_heads + kvh) * TILE);
-#pragma unroll
-            for (int i = 0; i < KI; ++i) c = M::qk(kp[64 * i + lane], qb[i], c);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int pos = lbs[b] * kBlock + 4 * g + j;
-            s[b][j] = (blk[b] >= 0 && pos < limit) ? c[j] * scale_log2 : -INFINITY;
-        }
-    }
-
-    // Exact per-wave row max: own scores, then the 4 lane groups.
-    float m = -INFINITY;
-#pragma unroll
-    for (int b = 0; b < NB; ++b)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) m = fmaxf(m, s[b][j]);
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
-
-    // O += P . V; P rounded to the operand type, and l sums the rounded P.
+    float m = -INFINITY, lsum = 0.f;
     f32x4 acc[VN];
 #pragma unroll
     for (int k = 0; k < VN; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
-    float lsum = 0.f;
+
+    if (nvalid > 0) {
+        int64_t first = 0;
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-        if (blk[b] < 0) continue;
-        x4 pa;
+        for (int b = NB - 1; b >= 0; --b)
+            if (ok[b]) first = blk[b];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const T ph = (T)(m == -INFINITY ? 0.f : exp2f(s[b][j] - m));
-            pa[j] = ph;
-            lsum += (float)ph;
-        }
-        const T *vt = v_pool + (blk[b] * num_kv_heads + kvh) * TILE;
-        // Tokens past the context in the last block hold stale bytes (maybe
-        // NaN); zero them so p = 0 contributes exactly nothing.
-        const int valid = ctx - lbs[b] * kBlock;
+        for (int b = 0; b < NB; ++b)
+            if (!ok[b]) blk[b] = first;
+
+        // Software pipeline over the wave's 2*NB tile loads (K tiles of
+        // blocks 0..NB-1, then V tiles): load stage t + PD is issued before
+        // stage t is consumed, and scheduling barriers keep the compiler from
+        // sinking the loads next to their uses.
+        x8 kb[NB][KI];
+        x4 vb[NB][VN];
+        auto issue = [&](int t) {
+            if (t < NB) {
+                const x8 *kp = reinterpret_cast<const x8 *>(k_pool + (blk[t] * num_kv_heads + kvh) * TILE);
 #pragma unroll
-        for (int k = 0; k < VN; ++k) {
-            x4 vv = *reinterpret_cast<const x4 *>(vt + (16 * k + n) * kBlock + 4 * g);
-            if (valid < kBlock) {
+                for (int i = 0; i < KI; ++i) kb[t][i] = stream_load(kp + 64 * i + lane);
+            } else if (t < 2 * NB) {
+                const T *vt = v_pool + (blk[t - NB] * num_kv_heads + kvh) * TILE;
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (4 * g + e >= valid) vv[e] = T(0.f);
+                for (int k = 0; k < VN; ++k)
+                    vb[t - NB][k] = stream_load(reinterpret_cast<const x4 *>(vt + (16 * k + n) * kBlock + 4 * g));
             }
-            acc[k] = M::pv(pa, vv, acc[k]);
+        };
+#pragma unroll
+        for (int t = 0; t < PD; ++t) issue(t);
+
+        // Scores S^T: s[b][j] = row n, token 4g + j of block b.
+        float s[NB][4];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            issue(b + PD);
+            __builtin_amdgcn_sched_barrier(0);
+            f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < KI; ++i) c = M::qk(kb[b][i], qb[i], c);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pos = lbs[b] * kBlock + 4 * g + j;
+                s[b][j] = (ok[b] && pos < limit) ? c[j] * scale_log2 : -INFINITY;
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // Exact per-wave row max: own scores, then the 4 lane groups.
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m = fmaxf(m, s[b][j]);
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+
+        // O += P . V; P rounded to the operand type, and l sums the rounded P.
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            issue(NB + b + PD);
+            __builtin_amdgcn_sched_barrier(0);
+            x4 pa;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const T ph = (T)(m == -INFINITY ? 0.f : exp2f(s[b][j] - m));
+                pa[j] = ph;
+                lsum += (float)ph;
+            }
+            // Tokens past the context hold stale bytes (maybe NaN), and masked
+            // blocks hold another block's bytes: zero them so p = 0 contributes
+            // exactly nothing.
+            const int valid = ok[b] ? ctx - lbs[b] * kBlock : 0;
+#pragma unroll
+            for (int k = 0; k < VN; ++k) {
+                x4 vv = vb[b][k];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) vv[e] = (4 * g + e < valid) ? vv[e] : T(0.f);
+                acc[k] = M::pv(pa, vv, acc[k]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
     lsum += __shfl_xor(lsum, 16);
@@ -305,7 +383,12 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
     __shared__ float o_lds[NW][ROWS][D];
     __shared__ float ml_lds[NW][ROWS][2];
 
-    const int part = blockIdx.x, kvh = blockIdx.y, seq = blockIdx.z;
+    // blockIdx.x = seq * num_kv_heads + kv head, blockIdx.y = partition: the
+    // dispatcher deals consecutive work-groups to the 8 XCDs round-robin, so
+    // with the (sequence, head) pair fastest every XCD gets the same mix of
+    // full and ragged partitions (partition-fastest would pin each XCD to one
+    // partition index, and late partitions exist only for long contexts).
+    const int part = blockIdx.y, kvh = blockIdx.x % num_kv_heads, seq = blockIdx.x / num_kv_heads;
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
     const int nparts = parts_of(ctx, P);
     if (part >= nparts) return;
@@ -457,10 +540,15 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2: log-sum-exp merge of a sequence's partitions, one wave per query row.
+// Pass 2: log-sum-exp merge of a sequence's partitions.  One wave per query
+// row, 4 rows per work-group: lane p owns partition p's (m, l) and weight
+// 2^(m_p - M); the partial rows are then streamed with the weight broadcast
+// from its lane, 8 partitions' loads in flight at a time.
 // ---------------------------------------------------------------------------
+constexpr int kCombineRows = 4;
+
 template <int D>
-__global__ __launch_bounds__(64) void paged_attn_combine_kernel(
+__global__ __launch_bounds__(64 * kCombineRows) void paged_attn_combine_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
     const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
     int max_blocks, int partition, int max_parts) {
@@ -468,9 +556,10 @@ __global__ __launch_bounds__(64) void paged_attn_combine_kernel(
     const int seq = blockIdx.y;
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
     const int nparts = parts_of(ctx, partition);
-    if (nparts == 1) return;
-    const int lane = threadIdx.x;
-    const int64_t row = (int64_t)seq * rows_per_seq + blockIdx.x;
+    const int r = blockIdx.x * kCombineRows + (threadIdx.x >> 6);
+    if (nparts == 1 || r >= rows_per_seq) return;
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)seq * rows_per_seq + r;
     const float *ml = ws_ml + 2 * row * max_parts;
     const float *o = ws_o + row * max_parts * D;
 
@@ -482,13 +571,21 @@ __global__ __launch_bounds__(64) void paged_attn_combine_kernel(
 #pragma unroll
     for (int k = 0; k < DPL; ++k) O[k] = 0.f;
     if (M != -INFINITY) {
-        for (int p = 0; p < nparts; ++p) {
-            const float mp = ml[2 * p];
-            const float f = mp == -INFINITY ? 0.f : exp2f(mp - M);
-            L = fmaf(f, ml[2 * p + 1], L);
+        for (int base = 0; base < nparts; base += 64) {
+            const int p = base + lane;
+            const float mp = p < nparts ? ml[2 * p] : -INFINITY;
+            const float wp = mp == -INFINITY ? 0.f : exp2f(mp - M);
+            if (p < nparts) L = fmaf(wp, ml[2 * p + 1], L);
+            const int cnt = min(64, nparts - base);
+            const float *ob = o + (int64_t)base * D + lane;
+#pragma unroll 8
+            for (int i = 0; i < cnt; ++i) {
+                const float w = __shfl(wp, i);
 #pragma unroll
-            for (int k = 0; k < DPL; ++k) O[k] = fmaf(f, o[(int64_t)p * D + lane + 64 * k], O[k]);
+                for (int k = 0; k < DPL; ++k) O[k] = fmaf(w, ob[(int64_t)i * D + 64 * k], O[k]);
+            }
         }
+        L = xor_sum<64>(L);
     }
 #pragma unroll
     for (int k = 0; k < DPL; ++k)
@@ -529,14 +626,15 @@ int launch_pair(const Args &a, PartitionKernel<T> kernel, int nw, int partition)
         ws_o = static_cast<float *>(a.workspace);
         ws_ml = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + a.ws_o_bytes);
     }
-    dim3 grid((unsigned)max_parts, (unsigned)a.Hkv, (unsigned)a.B);
+    dim3 grid((unsigned)(a.B * a.Hkv), (unsigned)max_parts);
     hipLaunchKernelGGL(kernel, grid, dim3(nw * 64), 0, a.stream, a.out, a.out_dtype,
                        static_cast<const T *>(a.q), static_cast<const T *>(a.k_pool),
                        static_cast<const T *>(a.v_pool), a.tables, a.ctx_lens, a.Hq, a.Hkv,
                        a.max_blocks, a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
     if (max_parts > 1)
-        hipLaunchKernelGGL(paged_attn_combine_kernel<D>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
-                           dim3(64), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
+        hipLaunchKernelGGL(paged_attn_combine_kernel<D>,
+                           dim3((unsigned)dlmk::ceil_div(a.NQ * a.Hq, kCombineRows), (unsigned)a.B),
+                           dim3(64 * kCombineRows), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
                            a.NQ * a.Hq, a.max_blocks, partition, max_parts);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
@@ -544,11 +642,12 @@ int launch_pair(const Args &a, PartitionKernel<T> kernel, int nw, int partition)
     return DLMK_OK;
 }
 
-// Matrix-core path: 4 waves x 8 blocks = 512-token partitions.
+// Matrix-core path: NW waves x NB blocks per partition.
 template <typename T, int D, int GQA, int NQ>
 int launch_mfma(const Args &a) {
-    constexpr int NW = 4, NB = 8;
-    return launch_pair<T, D>(a, &paged_attn_mfma_kernel<T, D, GQA, NQ, NW, NB>, NW,
+    constexpr int NW = DLMK_MFMA_NW, NB = DLMK_MFMA_NB, PD = DLMK_MFMA_PD;
+    static_assert(NW * NB * kBlock >= kMinPartition, "partition below the workspace bound");
+    return launch_pair<T, D>(a, &paged_attn_mfma_kernel<T, D, GQA, NQ, NW, NB, PD>, NW,
                              NW * NB * kBlock);
 }
 
@@ -645,7 +744,8 @@ int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const vo
     if (out_dtype != DLMK_F32 && out_dtype != DLMK_F16 && out_dtype != DLMK_BF16)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_paged_decode_attention: bad out dtype %d",
                           out_dtype);
-    if (num_seqs > 65535 || num_kv_heads > 65535)
+    if ((int64_t)num_seqs * num_kv_heads > 0x7fffffff ||
+        parts_for(max_blocks_per_seq, kMinPartition) > 65535 || num_seqs > 65535)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED, "dlmk_paged_decode_attention: grid too large");
 
     Args a;
