@@ -98,12 +98,26 @@ def _declare(L):
 
 
 def dtype_code(dt) -> int:
+    """float32 -> F32, float16 -> F16; raw uint16 arrays are bf16 bit patterns."""
     dt = np.dtype(dt)
     if dt == np.float32:
         return F32
     if dt == np.float16:
         return F16
+    if dt == np.uint16:
+        return BF16
     raise ValueError(f"unsupported dtype {dt}")
+
+
+def bf16_bits(x) -> np.ndarray:
+    """float32 -> bf16 bit patterns (uint16), round to nearest even."""
+    u = np.ascontiguousarray(x, np.float32).view(np.uint32).astype(np.uint64)
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    return r
+
+
+def bf16_to_f32(bits) -> np.ndarray:
+    return (np.asarray(bits, np.uint16).astype(np.uint32) << 16).view(np.float32)
 
 
 # ---------------------------------------------------------------- RNG / f16

@@ -40,9 +40,31 @@ class Workload:
         return np.float32(1.0) / np.sqrt(np.float32(self.d))
 
 
+BF16_ATOL, BF16_RTOL = 1.6e-2, 8e-3  # bf16 KV: 8x the f16 bound (3 fewer mantissa bits)
+
+
+def _bf16(a):
+    from oracle.oracle import bf16_bits
+    return bf16_bits(a)
+
+
 def make_workload(rng, ctx, Hq, Hkv, d, dtype, nq=1, sigma=1.0, num_blocks=None, spare=8,
                   fill_nan=False, bs=16):
-    """Pools filled through the logical view: token p of seq s at table[s][p//bs]."""
+    """Pools filled through the logical view: token p of seq s at table[s][p//bs].
+
+    dtype "bf16" stores bf16 bit patterns in uint16 arrays (NumPy has no bf16)."""
+    if isinstance(dtype, str) and dtype == "bf16":
+        w = make_workload(rng, ctx, Hq, Hkv, d, np.float32, nq, sigma, num_blocks, spare,
+                          fill_nan, bs)
+        X = 8
+        nb = w.k_pool.shape[0]
+        # re-chunk K for 8-element (16-byte) bf16 chunks: [nb][Hkv][d/4][bs][4] -> logical -> [d/8][bs][8]
+        k = w.k_pool.transpose(0, 1, 3, 2, 4).reshape(nb, Hkv, bs, d)
+        k = k.reshape(nb, Hkv, bs, d // X, X).transpose(0, 1, 3, 2, 4)
+        w.k_pool = _bf16(np.ascontiguousarray(k))
+        w.v_pool = _bf16(w.v_pool)
+        w.q = _bf16(w.q)
+        return w
     ctx = np.asarray(ctx, np.int32)
     B = len(ctx)
     need = [-(-int(c) // bs) for c in ctx]
@@ -74,4 +96,8 @@ def make_workload(rng, ctx, Hq, Hkv, d, dtype, nq=1, sigma=1.0, num_blocks=None,
 
 
 def to_dev(torch, arr, device):
-    return torch.from_numpy(np.ascontiguousarray(arr)).to(device)
+    """NumPy -> device tensor; uint16 arrays become bfloat16 (bit patterns kept)."""
+    arr = np.ascontiguousarray(arr)
+    if arr.dtype == np.uint16:
+        return torch.from_numpy(arr.view(np.int16)).to(device).view(torch.bfloat16)
+    return torch.from_numpy(arr).to(device)

@@ -5,8 +5,8 @@ dlm's attention() (src/forward/cpu.rs:1126-1151)."""
 import numpy as np
 import pytest
 
-from helpers import (F16_ATOL, F16_RTOL, F32_ATOL, F32_RTOL, assert_close, make_workload,
-                     to_dev)
+from helpers import (BF16_ATOL, BF16_RTOL, F16_ATOL, F16_RTOL, F32_ATOL, F32_RTOL, assert_close,
+                     make_workload, to_dev)
 
 pytestmark = pytest.mark.gpu
 
@@ -126,20 +126,30 @@ EDGE_CTX = [0, 1, 2, 15, 16, 17, 255, 256, 257, 511, 513, 1000]
     (np.float16, 8, 8, 128, 4, [4, 2, 513, 260]),           # 4-query verify, group 1
     (np.float16, 32, 8, 128, 2, [2, 257, 1025]),            # 2-query verify, group 4
     (np.float32, 16, 8, 64, 4, [5, 3, 400]),
+    (np.float16, 32, 8, 128, 4, [4, 1030, 2100, 700]),      # config-5 verify: 4 queries x GQA 4
+    (np.float16, 64, 8, 128, 2, [2, 600, 1500]),            # 2 queries x GQA 8
+    (np.float16, 32, 2, 128, 1, [300, 1200]),               # GQA 16
+    (np.float16, 16, 4, 256, 1, [17, 900]),                 # head_dim 256
+    (np.float16, 16, 4, 256, 2, [2, 530]),
+    ("bf16", 32, 8, 128, 1, EDGE_CTX),                      # bf16 KV, 8B shape
+    ("bf16", 32, 8, 128, 4, [4, 777]),
+    ("bf16", 16, 8, 64, 1, [33, 600]),
 ])
 def test_paged_attention_matches_oracle(oracle, torch_mod, ops, cuda, dtype, Hq, Hkv, d, nq,
                                         ctx):
-    banner(f"attention dtype={np.dtype(dtype).name} Hq={Hq} Hkv={Hkv} d={d} nq={nq} ctx={ctx}")
+    name = dtype if isinstance(dtype, str) else np.dtype(dtype).name
+    banner(f"attention dtype={name} Hq={Hq} Hkv={Hkv} d={d} nq={nq} ctx={ctx}")
     rng = np.random.default_rng(sum(ctx) + Hq + nq)
-    sigma = 0.5 if dtype == np.float16 else 1.0
+    sigma = 1.0 if dtype is np.float32 else 0.5
     w = make_workload(rng, ctx, Hq, Hkv, d, dtype, nq=nq, sigma=sigma)
     ref = oracle_attention(oracle, w)
-    atol, rtol = (F16_ATOL, F16_RTOL) if dtype == np.float16 else (F32_ATOL, F32_RTOL)
+    atol, rtol = {"float16": (F16_ATOL, F16_RTOL), "float32": (F32_ATOL, F32_RTOL),
+                  "bf16": (BF16_ATOL, BF16_RTOL)}[name]
     got = run_attention(torch_mod, ops, cuda, w, out_dtype=torch_mod.float32)
     assert_close(got, ref, atol, rtol, "f32 out")
-    if dtype == np.float16:
-        got16 = run_attention(torch_mod, ops, cuda, w)
-        assert_close(got16, ref, atol, rtol, "f16 out")
+    if name != "float32":
+        got16 = run_attention(torch_mod, ops, cuda, w)  # out in the KV dtype
+        assert_close(got16, ref, atol, rtol, f"{name} out")
 
 
 def test_paged_attention_ignores_stale_block_tails(oracle, torch_mod, ops, cuda):

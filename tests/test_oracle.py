@@ -255,3 +255,20 @@ def test_quantize_i4_round_trips_within_a_quantum(oracle):
     # round half away from zero (f32::round): 0.5 * scale -> code 1, -0.5 -> -1
     p2, s2 = oracle.quantize_i4(np.array([7.0, 0.5, -0.5], np.float32))
     assert [oracle.read_i4(p2, 0, i) for i in range(3)] == [7.0, 1.0, -1.0]
+
+
+def test_bf16_decode_matches_torch(oracle):
+    """The oracle's bf16 widening (used for bf16 pools) equals torch's bf16 -> f32."""
+    import torch
+    bits = np.arange(0, 65536, 7, dtype=np.uint16)
+    ref = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).float().numpy()
+    n = len(bits) - len(bits) % 128
+    v = bits[:n].reshape(-1, 1, 8, 16)  # [blocks][1 head][d=8][16]
+    k = np.zeros((v.shape[0], 1, 1, 16, 8), np.uint16)
+    table = np.arange(v.shape[0], dtype=np.int32)
+    _, vals = oracle.gather_logical(k, v, table, v.shape[0] * 16, 1, 8, 16, np.uint16)
+    got = vals.reshape(v.shape[0], 16, 8).transpose(0, 2, 1).reshape(-1)
+    finite = np.isfinite(ref[:n])
+    assert np.array_equal(got[finite], ref[:n][finite])
+    assert np.array_equal(np.isnan(got), np.isnan(ref[:n]))
+    assert np.array_equal(oracle.bf16_bits(ref[:n][finite]), bits[:n][finite])
