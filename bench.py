@@ -1,18 +1,23 @@
-"""Benchmark: paged KV append + paged GQA decode attention, Llama-3-8B shape, 1 GPU.
+"""Benchmark: paged KV append + paged GQA decode attention on one MI355X.
 
-Workload: one layer, 32 query heads, 8 KV heads,
-head_dim 128, f16 K/V/Q ~ N(0,1)*0.5, block_size 16; 64 sequences with
-contexts uniform in [128, 4096] (seeded) on non-contiguous blocks of a shuffled
-20k-block pool.  One step = append 1 token per sequence + paged decode
-attention over the whole context.  Two disjoint batches alternate step by step
-so the bytes read per step come from HBM, not the 256 MB Infinity Cache.
+Default workload (the metric's configuration):
+one Llama-3-8B layer -- 32 query heads, 8 KV heads, head_dim 128, f16 K/V/Q ~
+N(0,1)*0.5, block_size 16; 64 sequences with contexts uniform in [128, 4096]
+(seeded) on non-contiguous blocks of a shuffled 20k-block pool.  One step =
+append 1 token per sequence + paged decode attention over the whole context.
+Two disjoint batches alternate step by step so the bytes a step reads come
+from HBM, not the 256 MB Infinity Cache.
 
-Prints one JSON line (see `result` below).  `value` is the whole step's
-algorithmic HBM bytes (attention + append) per second.  The roofline object
-covers the dominant kernel, the attention partition kernel; its duration is
-measured with HIP events on the stream the kernels run on.
+`--workload config1|config3|config4|config5` runs the other BASELINE.json
+configurations the same way (they are parity-test cases for the driver, and
+bench lines for the design notes).
 
-    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu-baseline]
+Prints one JSON line.  `value` is the whole step's algorithmic HBM bytes
+(attention + append) per second; `roofline` covers the dominant kernel
+(attention); timing is HIP events around replays of HIP graphs on the stream
+the kernels run on.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--workload config2]
 """
 from __future__ import annotations
 
@@ -21,32 +26,91 @@ import json
 import os
 import sys
 import time
+from dataclasses import dataclass, field
 
 import numpy as np
 
 HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E
-HQ, HKV, D, BS = 32, 8, 128, 16
-BATCH, CTX_LO, CTX_HI, POOL_BLOCKS, SEED = 64, 128, 4096, 20000, 2
+BS = 16
+SEED = 2
+METRIC = "paged decode-attn HBM GB/s (% of peak) + KV-append tokens/s, 8B shape, 1 GPU"
+
+
+@dataclass
+class Workload:
+    name: str
+    about: str
+    hq: int
+    hkv: int
+    d: int
+    dtype: str  # "f16" | "f32"
+    batch: int
+    ctx: tuple  # uniform [lo, hi]
+    nq: int = 1  # tokens appended and queried per sequence per step
+    layers: int = 1
+    prefill_seqs: int = 0  # chunked-prefill sequences appending alongside
+    prefill_chunk: int = 0
+    extras: list = field(default_factory=list)  # "fork", "swap"
+
+
+WORKLOADS = {
+    "config1": Workload("config1", "configs[0]: Llama-3.2-1B KV (16 layers, 32/8 heads, d 64, f32), "
+                        "one sequence at 512 + 32 tokens, 1 token appended per layer per step",
+                        32, 8, 64, "f32", 1, (544, 544), layers=16),
+    "config2": Workload("config2", "configs[1]: Llama-3-8B single layer, paged KV append + GQA decode "
+                        "attention, B=64, ctx U[128,4096]", 32, 8, 128, "f16", 64, (128, 4096)),
+    "config3": Workload("config3", "configs[2]: continuous batching, 8B shape: 48 decode sequences at "
+                        "U[256,8192] + 4 chunked-prefill sequences appending 512 tokens each per step",
+                        32, 8, 128, "f16", 48, (256, 8192), prefill_seqs=4, prefill_chunk=512),
+    "config4": Workload("config4", "configs[3]: Llama-3-70B single layer (64/8 heads), B=8 x 32768 "
+                        "tokens, split-K + LSE merge", 64, 8, 128, "f16", 8, (32768, 32768)),
+    "config5": Workload("config5", "configs[4]: speculative verify on the 8B shape, B=32, ctx "
+                        "U[1024,8192], 4 drafts appended + 4-query causal attention per step; "
+                        "fork of 8 sequences and 25% swap measured separately",
+                        32, 8, 128, "f16", 32, (1024, 8192), nq=4, extras=["fork", "swap"]),
+}
 
 
 def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=200, help="timed steps (a multiple of 20)")
+    p.add_argument("--steps", type=int, default=200, help="timed steps (rounded to a multiple of 20)")
     p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--workload", default="config2", choices=sorted(WORKLOADS))
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bound on the CPU baseline sample's work")
     p.add_argument("--copy-calibration", action="store_true",
-                   help="only run dlmk_copy_blocks over 4096 pairs of 32-KiB blocks in each of 2 pools (256 MiB read + "
-                        "256 MiB written per launch), to scale FETCH_SIZE/WRITE_SIZE counters")
+                   help="only run dlmk_copy_blocks over 4096 pairs of 32-KiB blocks in each of 2 "
+                        "pools (256 MiB read + 256 MiB written per launch), to scale "
+                        "FETCH_SIZE/WRITE_SIZE counters")
     return p.parse_args()
+
+
+def elem_bytes(w):
+    return 4 if w.dtype == "f32" else 2
+
+
+def attn_bytes(w, ctx, out_bytes):
+    """Algorithmic bytes of one attention launch: K+V read, Q read, out write,
+    block table and context lengths."""
+    ctx = np.asarray(ctx, np.int64)
+    eb = elem_bytes(w)
+    kv = int(ctx.sum()) * 2 * w.hkv * w.d * eb
+    qo = len(ctx) * w.nq * w.hq * w.d * (eb + out_bytes)
+    meta = int(((ctx + BS - 1) // BS).sum()) * 4 + len(ctx) * 4
+    return kv + qo + meta
+
+
+def append_bytes(w, n_tok):
+    """Per appended token: K+V read, the same written, and an 8-byte slot."""
+    return n_tok * (2 * (2 * w.hkv * w.d * elem_bytes(w)) + 8)
 
 
 def copy_calibration(torch, ops, steps):
     """A plain copy of known size: 4096 pairs of 32 KiB blocks in each of the K and V pools."""
     dev = torch.device("cuda:0")
-    nb, bb = 8192, HKV * BS * D * 2
+    nb, bb = 8192, 8 * BS * 128 * 2
     k = torch.zeros(nb * bb, dtype=torch.uint8, device=dev)
     v = torch.zeros_like(k)
     pairs = torch.stack([torch.arange(0, 4096), torch.arange(4096, 8192)], 1).int().to(dev)
@@ -57,50 +121,34 @@ def copy_calibration(torch, ops, steps):
                                            "bytes_written_per_launch": 2 * 4096 * bb}}))
 
 
-def attn_bytes(ctx, nq=1, out_bytes=2):
-    """Algorithmic bytes of one attention launch: K+V read, Q read, out write,
-    block table and context lengths."""
-    ctx = np.asarray(ctx, np.int64)
-    kv = int(ctx.sum()) * 2 * HKV * D * 2
-    qo = len(ctx) * nq * HQ * D * (2 + out_bytes)
-    meta = int(((ctx + BS - 1) // BS).sum()) * 4 + len(ctx) * 4
-    return kv + qo + meta
-
-
-def append_bytes(n_tok):
-    """Per appended token: K+V read (4096 B), written (4096 B), 8-byte slot."""
-    return n_tok * (2 * (2 * HKV * D * 2) + 8)
-
-
-def cpu_baseline(budget_s):
+def cpu_baseline(w, budget_s):
     """dlm's CPU attention path (the oracle restatement, 1 thread) on a bounded
-    sample of the same workload: as many config-2 sequences as fit budget_s."""
+    sample of the same workload: as many sequences as fit budget_s."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import oracle as orc
     orc.build()
     rng = np.random.default_rng(SEED + 1000)
-    ctx_all = rng.integers(CTX_LO, CTX_HI + 1, BATCH)
+    npdt = np.float32 if w.dtype == "f32" else np.float16
+    X = 16 // np.dtype(npdt).itemsize
     done_tok, done_seq, elapsed, nbytes = 0, 0, 0.0, 0
-    for c in ctx_all:
-        c = int(c)
+    while elapsed < budget_s and done_seq < 4096:
+        c = int(rng.integers(w.ctx[0], w.ctx[1] + 1))
         nb = -(-c // BS)
-        kp = (rng.standard_normal((nb, HKV, D // 8, BS, 8)) * 0.5).astype(np.float16)
-        vp = (rng.standard_normal((nb, HKV, D, BS)) * 0.5).astype(np.float16)
+        kp = (rng.standard_normal((nb, w.hkv, w.d // X, BS, X)) * 0.5).astype(npdt)
+        vp = (rng.standard_normal((nb, w.hkv, w.d, BS)) * 0.5).astype(npdt)
         table = rng.permutation(nb).astype(np.int32)[None]
-        q = (rng.standard_normal((1, 1, HQ, D)) * 0.5).astype(np.float16)
+        q = (rng.standard_normal((1, w.nq, w.hq, w.d)) * 0.5).astype(npdt)
         t0 = time.perf_counter()
-        orc.paged_attention(q, kp, vp, table, np.array([c], np.int32), 1, HQ, HKV, D, BS,
-                            1.0 / np.sqrt(D))
+        orc.paged_attention(q, kp, vp, table, np.array([c], np.int32), w.nq, w.hq, w.hkv, w.d, BS,
+                            1.0 / np.sqrt(w.d))
         elapsed += time.perf_counter() - t0
         done_tok += c
         done_seq += 1
-        nbytes += attn_bytes([c])
-        if elapsed >= budget_s:
-            break
+        nbytes += attn_bytes(w, [c], elem_bytes(w))
     return {
         "value": round(nbytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
         "sample": (f"oracle/oracle.c paged attention (f32 restatement of dlm attention(), "
-                   f"1 thread) over {done_seq} config-2 sequences, {done_tok} context tokens, "
+                   f"1 thread) over {done_seq} {w.name} sequences, {done_tok} context tokens, "
                    f"{elapsed:.1f} s; same algorithmic-bytes formula"),
         "context_tokens_per_s": round(done_tok / elapsed, 1),
         "cpu_model": _cpu_model(), "host_nproc": os.cpu_count(),
@@ -118,25 +166,32 @@ def _cpu_model():
 
 
 class Batch:
-    """One set of 64 sequences: books, device block tables, slots and inputs."""
+    """One set of sequences: books, device block tables, slots and inputs."""
 
-    def __init__(self, torch, cache, seq_base, ctx, dev, gen):
+    def __init__(self, torch, w, cache, seq_base, ctx, dev, gen, tdt):
         self.seqs = [seq_base + i for i in range(len(ctx))]
+        # Each sequence holds its context, the last nq tokens being this step's drafts.
         for s, c in zip(self.seqs, ctx):
-            cache.append_tokens(s, int(c))  # prefill + the token this step appends
-        max_blocks = -(-CTX_HI // BS)
+            cache.append_tokens(s, int(c))
+        max_blocks = -(-w.ctx[1] // BS)
         tables, lens = cache.block_tables(self.seqs, max_blocks)
-        slots = np.array([cache.slot_mapping(s, int(c) - 1, 1)[0] for s, c in zip(self.seqs, ctx)],
-                         np.int64)
+        slots = [cache.slot_mapping(s, int(c) - w.nq, w.nq) for s, c in zip(self.seqs, ctx)]
+        # Chunked-prefill sequences: their chunk of this step is appended alongside.
+        self.prefill = [seq_base + 500 + i for i in range(w.prefill_seqs)]
+        for s in self.prefill:
+            cache.append_tokens(s, w.prefill_chunk)
+            slots.append(cache.slot_mapping(s, 0, w.prefill_chunk))
+        slots = np.concatenate(slots).astype(np.int64)
+        self.n_append = len(slots)
         self.tables = torch.from_numpy(tables).to(dev)
         self.lens = torch.from_numpy(lens).to(dev)
         self.slots = torch.from_numpy(slots).to(dev)
         self.ctx = ctx
         n = len(ctx)
-        self.q = (torch.randn((n, 1, HQ, D), generator=gen, device=dev) * 0.5).half()
-        self.k_new = (torch.randn((n, HKV, D), generator=gen, device=dev) * 0.5).half()
-        self.v_new = (torch.randn((n, HKV, D), generator=gen, device=dev) * 0.5).half()
-        self.out = torch.empty((n, 1, HQ, D), dtype=torch.float16, device=dev)
+        self.q = (torch.randn((n, w.nq, w.hq, w.d), generator=gen, device=dev) * 0.5).to(tdt)
+        self.k_new = (torch.randn((self.n_append, w.hkv, w.d), generator=gen, device=dev) * 0.5).to(tdt)
+        self.v_new = (torch.randn((self.n_append, w.hkv, w.d), generator=gen, device=dev) * 0.5).to(tdt)
+        self.out = torch.empty((n, w.nq, w.hq, w.d), dtype=tdt, device=dev)
 
 
 def main():
@@ -154,49 +209,57 @@ def main():
     if args.copy_calibration:
         copy_calibration(torch, ops, args.steps)
         return
+    w = WORKLOADS[args.workload]
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev)
     gen.manual_seed(SEED)
+    tdt = torch.float32 if w.dtype == "f32" else torch.float16
 
-    cfg = KvCacheConfig(num_layers=1, num_kv_heads=HKV, head_dim=D, block_size=BS)
-    cache = PagedKvCache.with_seeded_shuffle(cfg, POOL_BLOCKS, seed=SEED)
-    geom = ops.PoolGeometry(POOL_BLOCKS, HKV, D, BS, torch.float16)
-    (k_pool, v_pool), = ops.alloc_pools(geom, dev)
-    k_pool.normal_(0.0, 0.5, generator=gen)
-    v_pool.normal_(0.0, 0.5, generator=gen)
-
+    # Pool: both batches (plus prefill chunks and fork room) with slack, shuffled.
     rng = np.random.default_rng(SEED)
-    batches = []
+    ctxs = [rng.integers(w.ctx[0], w.ctx[1] + 1, w.batch).astype(np.int32) for _ in range(2)]
+    need = sum(int(((c + BS - 1) // BS).sum()) for c in ctxs)
+    need += 2 * w.prefill_seqs * (-(-w.prefill_chunk // BS))
+    floor = 20000 if w.layers == 1 else 0  # configs[1] quotes a 20k-block pool
+    pool_blocks = max(floor, int(need * (1.6 if "fork" in w.extras else 1.2)) + 64)
+    cfg = KvCacheConfig(num_layers=w.layers, num_kv_heads=w.hkv, head_dim=w.d, block_size=BS)
+    cache = PagedKvCache.with_seeded_shuffle(cfg, pool_blocks, seed=SEED)
+    geom = ops.PoolGeometry(pool_blocks, w.hkv, w.d, BS, tdt)
+    layers = ops.alloc_pools(geom, dev, num_layers=w.layers)
+    for kp, vp in layers:
+        kp.normal_(0.0, 0.5, generator=gen)
+        vp.normal_(0.0, 0.5, generator=gen)
+
     t_books = time.perf_counter()
-    for b in range(2):
-        ctx = rng.integers(CTX_LO, CTX_HI + 1, BATCH).astype(np.int32)
-        batches.append(Batch(torch, cache, b * 1000, ctx, dev, gen))
+    batches = [Batch(torch, w, cache, b * 1000, ctxs[b], dev, gen, tdt) for b in range(2)]
     books_s = time.perf_counter() - t_books
-    ws = ops.alloc_workspace(ops.attention_workspace_bytes(BATCH, 1, HQ, D, -(-CTX_HI // BS)), dev)
+    max_blocks = -(-w.ctx[1] // BS)
+    ws = ops.alloc_workspace(ops.attention_workspace_bytes(w.batch, w.nq, w.hq, w.d, max_blocks), dev)
 
     def append(bt):
-        ops.kv_append(k_pool, v_pool, bt.k_new, bt.v_new, bt.slots, num_kv_heads=HKV,
-                      head_dim=D)
+        for kp, vp in layers:
+            ops.kv_append(kp, vp, bt.k_new, bt.v_new, bt.slots, num_kv_heads=w.hkv, head_dim=w.d)
 
     def attend(bt):
-        ops.paged_decode_attention(bt.q, k_pool, v_pool, bt.tables, bt.lens, num_kv_heads=HKV,
-                                   out=bt.out, workspace=ws)
+        for kp, vp in layers:
+            ops.paged_decode_attention(bt.q, kp, vp, bt.tables, bt.lens, num_kv_heads=w.hkv,
+                                       out=bt.out, workspace=ws)
 
-    def step(i):
-        bt = batches[i & 1]
-        append(bt)
-        attend(bt)
+    def step(bt):
+        # Per layer: append this step's tokens, then attend (dlm's per-layer order).
+        for kp, vp in layers:
+            ops.kv_append(kp, vp, bt.k_new, bt.v_new, bt.slots, num_kv_heads=w.hkv, head_dim=w.d)
+            ops.paged_decode_attention(bt.q, kp, vp, bt.tables, bt.lens, num_kv_heads=w.hkv,
+                                       out=bt.out, workspace=ws)
 
-    stream = torch.cuda.current_stream()
     for i in range(args.warmup):
-        step(i)
+        step(batches[i & 1])
     torch.cuda.synchronize()
 
-    # The timed work runs as HIP graphs (one per batch and per phase), the way
-    # a serving loop replays a fixed decode step: no host launch overhead in
-    # the measurement, only the kernels.  Every launch inside is a libdlmk
-    # kernel; nothing is captured that writes memory by memset.
+    # The timed work runs as HIP graphs, the way a serving loop replays a fixed
+    # decode step: no host launch overhead in the measurement, only kernels.
+    # Every launch inside is a libdlmk kernel; nothing writes memory by memset.
     def capture(fn, reps):
         """One graph holding `reps` launches of fn, alternating the two batches
         (amortises the graph launch itself over many kernels)."""
@@ -208,9 +271,6 @@ def main():
         return g
 
     REPS = 20
-    g_step = capture(lambda bt: (append(bt), attend(bt)), REPS)
-    g_attn = capture(attend, REPS)
-    g_app = capture(append, 5 * REPS)
     stream = torch.cuda.current_stream()
 
     def timed(graph, reps, n):
@@ -225,22 +285,23 @@ def main():
         torch.cuda.synchronize()
         return a.elapsed_time(b) / (reps * (n // reps))
 
-    # Whole steps.
     t0 = time.perf_counter()
-    step_ms = timed(g_step, REPS, args.steps)
+    step_ms = timed(capture(step, REPS), REPS, args.steps)
     wall_s = time.perf_counter() - t0
-    # Attention alone (the dominant kernel pair) and append alone.
-    attn_ms = timed(g_attn, REPS, args.steps)
-    append_ms = timed(g_app, 5 * REPS, 5 * args.steps)
+    attn_ms = timed(capture(attend, REPS), REPS, args.steps)
+    append_ms = timed(capture(append, 5 * REPS), 5 * REPS, 5 * args.steps)
 
-    mean_attn_bytes = (attn_bytes(batches[0].ctx) + attn_bytes(batches[1].ctx)) / 2
-    step_bytes = mean_attn_bytes + append_bytes(BATCH)
+    eb = elem_bytes(w)
+    L = w.layers
+    mean_attn_bytes = L * (attn_bytes(w, batches[0].ctx, eb) + attn_bytes(w, batches[1].ctx, eb)) / 2
+    n_app = (batches[0].n_append + batches[1].n_append) / 2
+    step_bytes = mean_attn_bytes + L * append_bytes(w, n_app)
     value = step_bytes / (step_ms * 1e-3) / 1e9
     attn_gbps = mean_attn_bytes / (attn_ms * 1e-3) / 1e9
     ctx_tok = (batches[0].ctx.sum() + batches[1].ctx.sum()) / 2
 
     result = {
-        "metric": "paged decode-attn HBM GB/s (% of peak) + KV-append tokens/s, 8B shape, 1 GPU",
+        "metric": METRIC,
         "value": round(value, 1),
         "unit": "GB/s",
         "n_gpus": 1,
@@ -250,41 +311,92 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f16",
+        "dtype": w.dtype,
         "data": "synthetic (seeded N(0,1)*0.5 K/V/Q, seeded contexts and shuffled pool)",
         "config": {
-            "workload": "configs[1]: Llama-3-8B single layer, paged KV append + GQA decode attention",
-            "num_q_heads": HQ, "num_kv_heads": HKV, "head_dim": D, "block_size": BS,
-            "batch": BATCH, "ctx": f"U[{CTX_LO},{CTX_HI}] seed {SEED}",
-            "pool_blocks": POOL_BLOCKS, "rotating_batches": 2,
-            "mean_context_tokens": float(ctx_tok),
-            "parallelism": "single GPU",
+            "workload": w.about,
+            "num_q_heads": w.hq, "num_kv_heads": w.hkv, "head_dim": w.d, "block_size": BS,
+            "layers": w.layers, "batch": w.batch, "queries_per_seq": w.nq,
+            "ctx": f"U[{w.ctx[0]},{w.ctx[1]}] seed {SEED}", "pool_blocks": pool_blocks,
+            "rotating_batches": 2, "mean_context_tokens": float(ctx_tok),
+            "appended_tokens_per_step": n_app, "parallelism": "single GPU",
         },
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
         "attention": {
             "GBps": round(attn_gbps, 1), "pct_of_hbm_peak": round(100 * attn_gbps / HBM_PEAK_GBPS, 2),
-            "us_per_launch": round(attn_ms * 1e3, 2),
-            "algorithmic_bytes_per_launch": int(mean_attn_bytes),
-            "context_tokens_per_s": round(ctx_tok / (attn_ms * 1e-3), 1),
-            "query_tokens_per_s": round(BATCH / (attn_ms * 1e-3), 1),
+            "us_per_launch": round(attn_ms * 1e3 / L, 2),
+            "algorithmic_bytes_per_launch": int(mean_attn_bytes / L),
+            "context_tokens_per_s": round(L * ctx_tok / (attn_ms * 1e-3), 1),
+            "query_tokens_per_s": round(w.batch * w.nq / (attn_ms * 1e-3), 1),
         },
         "kv_append": {
-            "tokens_per_s": round(BATCH / (append_ms * 1e-3), 1),
-            "us_per_launch": round(append_ms * 1e3, 2),
-            "GBps": round(append_bytes(BATCH) / (append_ms * 1e-3) / 1e9, 2),
+            "tokens_per_s": round(L * n_app / (append_ms * 1e-3), 1),
+            "us_per_launch": round(append_ms * 1e3 / L, 2),
+            "GBps": round(L * append_bytes(w, n_app) / (append_ms * 1e-3) / 1e9, 2),
         },
-        "host_books_s_for_128_seqs": round(books_s, 4),
+        "host_books_s": round(books_s, 4),
         "wall_s_timed_region": round(wall_s, 4),
-        "timing": "HIP events around replays of HIP graphs of 20 steps each (100 appends for the append-only line), alternating the two batches",
+        "timing": f"HIP events around replays of HIP graphs of {REPS} steps each ({5 * REPS} "
+                  "appends for the append-only line), alternating the two batches",
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
-            "kernel": "paged_attn_mfma_kernel + paged_attn_combine_kernel (one launch pair)",
+            "kernel": "paged_attn_mfma_kernel" if w.dtype != "f32" else "paged_attn_valu_kernel",
         },
     }
+    if "fork" in w.extras:
+        result["fork"] = bench_fork(torch, ops, cache, layers[0], batches[0], w)
+    if "swap" in w.extras:
+        result["swap"] = bench_swap(torch, ops, cache, layers[0], batches[0], w, dev)
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds)
+        result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
     print(json.dumps(result), flush=True)
+
+
+def _events(torch, fn, n):
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    fn()
+    torch.cuda.synchronize()
+    a.record()
+    for _ in range(n):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) / n
+
+
+def bench_fork(torch, ops, cache, pools, bt, w):
+    """Fork 8 sequences by block copy (dlmk_copy_blocks), K and V pools."""
+    pairs = np.concatenate([cache.fork_sequence(s, 10_000 + s) for s in bt.seqs[:8]])
+    bb = w.hkv * BS * w.d * elem_bytes(w)
+    p = torch.from_numpy(pairs).to(pools[0].device)
+    ms = _events(torch, lambda: ops.copy_blocks(pools[0], pools[1], p, bb), 20)
+    nbytes = 2 * 2 * len(pairs) * bb
+    return {"blocks": int(len(pairs)), "bytes_moved": nbytes, "us": round(ms * 1e3, 2),
+            "GBps": round(nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
+def bench_swap(torch, ops, cache, pools, bt, w, dev):
+    """Swap 25% of the batch's blocks out to pinned host memory and back:
+    gather/scatter kernels (HBM GB/s) and the PCIe copies (GB/s) separately."""
+    rng = np.random.default_rng(SEED + 5)
+    owned = np.array([b for s in bt.seqs for b in cache.block_table(s)], np.int32)
+    ids_np = rng.choice(owned, len(owned) // 4, replace=False).astype(np.int32)
+    ids = torch.from_numpy(ids_np).to(dev)
+    bb = w.hkv * BS * w.d * elem_bytes(w)
+    nbytes = 2 * len(ids_np) * bb
+    staging = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    host = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
+    g_ms = _events(torch, lambda: ops.gather_blocks(pools[0], pools[1], ids, bb, staging), 10)
+    s_ms = _events(torch, lambda: ops.scatter_blocks(pools[0], pools[1], staging, ids, bb), 10)
+    out_ms = _events(torch, lambda: ops.swap_out(host, pools[0], pools[1], ids, bb, staging), 5)
+    in_ms = _events(torch, lambda: ops.swap_in(pools[0], pools[1], host, ids, bb, staging), 5)
+    return {"blocks": int(len(ids_np)), "bytes": nbytes,
+            "gather_hbm_GBps": round(2 * nbytes / (g_ms * 1e-3) / 1e9, 1),
+            "scatter_hbm_GBps": round(2 * nbytes / (s_ms * 1e-3) / 1e9, 1),
+            "swap_out_us": round(out_ms * 1e3, 1), "swap_in_us": round(in_ms * 1e3, 1),
+            "swap_out_pcie_GBps": round(nbytes / (out_ms * 1e-3) / 1e9, 1),
+            "swap_in_pcie_GBps": round(nbytes / (in_ms * 1e-3) / 1e9, 1)}
 
 
 if __name__ == "__main__":
