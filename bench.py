@@ -75,9 +75,12 @@ def parse():
     p = argparse.ArgumentParser()
     p.add_argument("--gpus", type=int, default=1)
     p.add_argument("--steps", type=int, default=200, help="timed steps (rounded to a multiple of 20)")
-    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=500,
+                   help="untimed steps run before each timed region (lets clocks settle)")
     p.add_argument("--workload", default="config2", choices=sorted(WORKLOADS))
     p.add_argument("--no-cpu-baseline", action="store_true")
+    p.add_argument("--only", choices=["step", "unfused", "attention", "append"],
+                   help="time one phase only (for profiling runs)")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bound on the CPU baseline sample's work")
     p.add_argument("--copy-calibration", action="store_true",
@@ -192,6 +195,11 @@ class Batch:
         self.k_new = (torch.randn((self.n_append, w.hkv, w.d), generator=gen, device=dev) * 0.5).to(tdt)
         self.v_new = (torch.randn((self.n_append, w.hkv, w.d), generator=gen, device=dev) * 0.5).to(tdt)
         self.out = torch.empty((n, w.nq, w.hq, w.d), dtype=tdt, device=dev)
+        # The decode sequences' tokens come first: [B][nq][Hkv][d] for the fused
+        # step; the prefill chunks (if any) follow and are appended on their own.
+        nd = n * w.nq
+        self.k_dec, self.v_dec = self.k_new[:nd], self.v_new[:nd]
+        self.k_pre, self.v_pre, self.slots_pre = self.k_new[nd:], self.v_new[nd:], self.slots[nd:]
 
 
 def main():
@@ -246,12 +254,22 @@ def main():
             ops.paged_decode_attention(bt.q, kp, vp, bt.tables, bt.lens, num_kv_heads=w.hkv,
                                        out=bt.out, workspace=ws)
 
-    def step(bt):
+    def step_unfused(bt):
         # Per layer: append this step's tokens, then attend (dlm's per-layer order).
         for kp, vp in layers:
             ops.kv_append(kp, vp, bt.k_new, bt.v_new, bt.slots, num_kv_heads=w.hkv, head_dim=w.d)
             ops.paged_decode_attention(bt.q, kp, vp, bt.tables, bt.lens, num_kv_heads=w.hkv,
                                        out=bt.out, workspace=ws)
+
+    def step(bt):
+        # Per layer: the fused decode step appends the decode tokens and attends
+        # in one launch; chunked-prefill tokens are appended alongside.
+        for kp, vp in layers:
+            if bt.slots_pre.numel():
+                ops.kv_append(kp, vp, bt.k_pre, bt.v_pre, bt.slots_pre, num_kv_heads=w.hkv,
+                              head_dim=w.d)
+            ops.paged_decode_step(bt.q, bt.k_dec, bt.v_dec, kp, vp, bt.tables, bt.lens,
+                                  num_kv_heads=w.hkv, out=bt.out, workspace=ws)
 
     for i in range(args.warmup):
         step(batches[i & 1])
@@ -274,7 +292,7 @@ def main():
     stream = torch.cuda.current_stream()
 
     def timed(graph, reps, n):
-        for _ in range(max(1, args.warmup // reps)):
+        for _ in range(max(1, -(-args.warmup // reps))):
             graph.replay()
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda.synchronize()
@@ -285,11 +303,17 @@ def main():
         torch.cuda.synchronize()
         return a.elapsed_time(b) / (reps * (n // reps))
 
+    def phase(name, fn, reps, n):
+        if args.only not in (None, name):
+            return float("nan")
+        return timed(capture(fn, reps), reps, n)
+
     t0 = time.perf_counter()
-    step_ms = timed(capture(step, REPS), REPS, args.steps)
+    step_ms = phase("step", step, REPS, args.steps)
     wall_s = time.perf_counter() - t0
-    attn_ms = timed(capture(attend, REPS), REPS, args.steps)
-    append_ms = timed(capture(append, 5 * REPS), 5 * REPS, 5 * args.steps)
+    unfused_ms = phase("unfused", step_unfused, REPS, args.steps)
+    attn_ms = phase("attention", attend, REPS, args.steps)
+    append_ms = phase("append", append, 5 * REPS, 5 * args.steps)
 
     eb = elem_bytes(w)
     L = w.layers
@@ -308,6 +332,7 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(step_ms, 5),
+        "ms_per_step_unfused": round(unfused_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -337,7 +362,10 @@ def main():
         "host_books_s": round(books_s, 4),
         "wall_s_timed_region": round(wall_s, 4),
         "timing": f"HIP events around replays of HIP graphs of {REPS} steps each ({5 * REPS} "
-                  "appends for the append-only line), alternating the two batches",
+                  "appends for the append-only line), alternating the two batches; a step is "
+                  "dlmk_paged_decode_step (append + attention in one launch), "
+                  "ms_per_step_unfused the same step as dlmk_kv_append + "
+                  "dlmk_paged_decode_attention",
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,

@@ -70,6 +70,8 @@ SIGNATURES = {
     "dlmk_paged_decode_attention": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _i32,
                                            _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _vp,
                                            _sz]),
+    "dlmk_paged_decode_step": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32,
+                                      _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _vp, _sz]),
     "dlmk_copy_blocks": (_i32, [_vp, _vp, _vp, _vp, _i64, _sz, _i64]),
     "dlmk_gather_blocks": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _sz, _i64]),
     "dlmk_scatter_blocks": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _sz, _i64]),

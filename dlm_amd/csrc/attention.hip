@@ -143,6 +143,35 @@ __device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][D],
     }
 }
 
+// Fused decode step: the wave that owns block `blk` (logical block `lb`) of a
+// sequence writes the sequence's newest positions ctx - nq .. ctx - 1 that
+// fall in that block -- its kv head's K and V, the same bits dlmk_kv_append
+// would write -- before it loads the block.  Only this wave reads that tile
+// in the launch, and the lanes of one wavefront see each other's global
+// stores in program order, so a wavefront-scope fence is all the ordering
+// needed (no work-group barrier on the critical path).
+template <typename T, int D>
+__device__ __forceinline__ void append_new_in_block(T *k_pool, T *v_pool, const T *k_new,
+                                                    const T *v_new, int64_t blk, int lb, int seq,
+                                                    int kvh, int num_kv_heads, int nq, int ctx,
+                                                    int lane) {
+    constexpr int X = 16 / sizeof(T);
+    constexpr int TILE = D * kBlock;
+    const int lo = max(ctx - nq, lb * kBlock), hi = min(ctx, lb * kBlock + kBlock);
+    const int64_t base = (blk * num_kv_heads + kvh) * TILE;
+    for (int e = lane; e < (hi - lo) * D; e += 64) {
+        const int p = lo + e / D, dim = e % D;
+        const int t = p - lb * kBlock, j = p - (ctx - nq);
+        const int64_t src = ((int64_t)(seq * nq + j) * num_kv_heads + kvh) * D + dim;
+        k_pool[base + (dim / X * kBlock + t) * X + dim % X] = k_new[src];
+        v_pool[base + dim * kBlock + t] = v_new[src];
+    }
+}
+
+__device__ __forceinline__ bool holds_new(int lb, int ctx, int nq) {
+    return lb * kBlock < ctx && lb * kBlock + kBlock > ctx - nq;
+}
+
 // ---------------------------------------------------------------------------
 // Matrix-core partition kernel (f16 / bf16 pools).
 // ---------------------------------------------------------------------------
@@ -183,8 +212,8 @@ struct Mfma<__bf16> {
 
 template <typename T, int D, int GQA, int NQ, int NW, int NB, int PD>
 __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kernel(
-    void *__restrict__ out, int out_dtype, const T *__restrict__ q,
-    const T *__restrict__ k_pool, const T *__restrict__ v_pool,
+    void *__restrict__ out, int out_dtype, const T *__restrict__ q, T *__restrict__ k_pool,
+    T *__restrict__ v_pool, const T *__restrict__ k_new, const T *__restrict__ v_new,
     const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
     int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
     int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
@@ -253,6 +282,16 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     f32x4 acc[VN];
 #pragma unroll
     for (int k = 0; k < VN; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    if (k_new != nullptr) {
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            if (ok[b] && holds_new(lbs[b], ctx, NQ))
+                append_new_in_block<T, D>(k_pool, v_pool, k_new, v_new, blk[b], lbs[b], seq, kvh,
+                                          num_kv_heads, NQ, ctx, lane);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
 
     if (nvalid > 0) {
         int64_t first = 0;
@@ -364,8 +403,8 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
 // ---------------------------------------------------------------------------
 template <int D, int GQA, int NQ, int NW>
 __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
-    void *__restrict__ out, int out_dtype, const float *__restrict__ q,
-    const float *__restrict__ k_pool, const float *__restrict__ v_pool,
+    void *__restrict__ out, int out_dtype, const float *__restrict__ q, float *__restrict__ k_pool,
+    float *__restrict__ v_pool, const float *__restrict__ k_new, const float *__restrict__ v_new,
     const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
     int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
     int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
@@ -405,6 +444,15 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
         const int lb = first_lb + b;
         int64_t id = lb < nblk_seq ? (int64_t)table[lb] : -1;
         blk[b] = (id >= 0 && id < num_blocks) ? id : -1;
+    }
+    if (k_new != nullptr) {
+#pragma unroll
+        for (int b = 0; b < BPW; ++b)
+            if (blk[b] >= 0 && holds_new(first_lb + b, ctx, NQ))
+                append_new_in_block<float, D>(k_pool, v_pool, k_new, v_new, blk[b], first_lb + b,
+                                              seq, kvh, num_kv_heads, NQ, ctx, lane);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     }
 
     uint4 kb[BPW][KI], vb[BPW][KI];
@@ -540,56 +588,67 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2: log-sum-exp merge of a sequence's partitions.  One wave per query
-// row, 4 rows per work-group: lane p owns partition p's (m, l) and weight
-// 2^(m_p - M); the partial rows are then streamed with the weight broadcast
-// from its lane, 8 partitions' loads in flight at a time.
+// Pass 2: log-sum-exp merge of a sequence's partitions.  One work-group per
+// (query row, sequence): the block reduces the partitions' max M, then wave w
+// accumulates partitions w, w + W, ... (every load independent, so many are
+// in flight), and the W partial sums meet in LDS.
 // ---------------------------------------------------------------------------
-constexpr int kCombineRows = 4;
+constexpr int kCombineWaves = 4;
 
 template <int D>
-__global__ __launch_bounds__(64 * kCombineRows) void paged_attn_combine_kernel(
+__global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
     const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
     int max_blocks, int partition, int max_parts) {
+    constexpr int W = kCombineWaves;
     constexpr int DPL = D / 64;  // dims per lane
+    __shared__ float red[W];
+    __shared__ float so[W][D + 1];
     const int seq = blockIdx.y;
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
     const int nparts = parts_of(ctx, partition);
-    const int r = blockIdx.x * kCombineRows + (threadIdx.x >> 6);
-    if (nparts == 1 || r >= rows_per_seq) return;
-    const int lane = threadIdx.x & 63;
-    const int64_t row = (int64_t)seq * rows_per_seq + r;
+    if (nparts == 1) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row = (int64_t)seq * rows_per_seq + blockIdx.x;
     const float *ml = ws_ml + 2 * row * max_parts;
     const float *o = ws_o + row * max_parts * D;
 
     float M = -INFINITY;
-    for (int p = lane; p < nparts; p += 64) M = fmaxf(M, ml[2 * p]);
+    for (int p = threadIdx.x; p < nparts; p += 64 * W) M = fmaxf(M, ml[2 * p]);
     M = xor_max<64>(M);
+    if (lane == 0) red[wave] = M;
+    __syncthreads();
+    M = red[0];
+#pragma unroll
+    for (int w = 1; w < W; ++w) M = fmaxf(M, red[w]);
 
     float O[DPL], L = 0.f;
 #pragma unroll
     for (int k = 0; k < DPL; ++k) O[k] = 0.f;
     if (M != -INFINITY) {
-        for (int base = 0; base < nparts; base += 64) {
-            const int p = base + lane;
-            const float mp = p < nparts ? ml[2 * p] : -INFINITY;
-            const float wp = mp == -INFINITY ? 0.f : exp2f(mp - M);
-            if (p < nparts) L = fmaf(wp, ml[2 * p + 1], L);
-            const int cnt = min(64, nparts - base);
-            const float *ob = o + (int64_t)base * D + lane;
-#pragma unroll 8
-            for (int i = 0; i < cnt; ++i) {
-                const float w = __shfl(wp, i);
+#pragma unroll 4
+        for (int p = wave; p < nparts; p += W) {
+            const float mp = ml[2 * p];
+            const float f = mp == -INFINITY ? 0.f : exp2f(mp - M);
+            L = fmaf(f, ml[2 * p + 1], L);
 #pragma unroll
-                for (int k = 0; k < DPL; ++k) O[k] = fmaf(w, ob[(int64_t)i * D + 64 * k], O[k]);
-            }
+            for (int k = 0; k < DPL; ++k) O[k] = fmaf(f, o[(int64_t)p * D + lane + 64 * k], O[k]);
         }
-        L = xor_sum<64>(L);
     }
+    __syncthreads();  // red[] reads done before it is reused for L
 #pragma unroll
-    for (int k = 0; k < DPL; ++k)
-        store_out(out, out_dtype, row * D + lane + 64 * k, L > 0.f ? O[k] / L : 0.f);
+    for (int k = 0; k < DPL; ++k) so[wave][lane + 64 * k] = O[k];
+    if (lane == 0) red[wave] = L;
+    __syncthreads();
+    float Lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) Lt += red[w];
+    for (int d = threadIdx.x; d < D; d += 64 * W) {
+        float Ot = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) Ot += so[w][d];
+        store_out(out, out_dtype, row * D + d, Lt > 0.f ? Ot / Lt : 0.f);
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -598,7 +657,9 @@ __global__ __launch_bounds__(64 * kCombineRows) void paged_attn_combine_kernel(
 struct Args {
     void *out;
     int out_dtype;
-    const void *q, *k_pool, *v_pool;
+    const void *q;
+    void *k_pool, *v_pool;
+    const void *k_new, *v_new;  // fused decode step: tokens appended in the same launch
     const int32_t *tables, *ctx_lens;
     int B, NQ, Hq, Hkv, max_blocks;
     int64_t num_blocks;
@@ -614,9 +675,9 @@ int64_t parts_for(int max_blocks, int partition) {
 }
 
 template <typename T>
-using PartitionKernel = void (*)(void *, int, const T *, const T *, const T *, const int32_t *,
-                                 const int32_t *, int, int, int, int64_t, float, int, float *,
-                                 float *);
+using PartitionKernel = void (*)(void *, int, const T *, T *, T *, const T *, const T *,
+                                 const int32_t *, const int32_t *, int, int, int, int64_t, float,
+                                 int, float *, float *);
 
 template <typename T, int D>
 int launch_pair(const Args &a, PartitionKernel<T> kernel, int nw, int partition) {
@@ -628,13 +689,13 @@ int launch_pair(const Args &a, PartitionKernel<T> kernel, int nw, int partition)
     }
     dim3 grid((unsigned)(a.B * a.Hkv), (unsigned)max_parts);
     hipLaunchKernelGGL(kernel, grid, dim3(nw * 64), 0, a.stream, a.out, a.out_dtype,
-                       static_cast<const T *>(a.q), static_cast<const T *>(a.k_pool),
-                       static_cast<const T *>(a.v_pool), a.tables, a.ctx_lens, a.Hq, a.Hkv,
+                       static_cast<const T *>(a.q), static_cast<T *>(a.k_pool),
+                       static_cast<T *>(a.v_pool), static_cast<const T *>(a.k_new),
+                       static_cast<const T *>(a.v_new), a.tables, a.ctx_lens, a.Hq, a.Hkv,
                        a.max_blocks, a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
     if (max_parts > 1)
-        hipLaunchKernelGGL(paged_attn_combine_kernel<D>,
-                           dim3((unsigned)dlmk::ceil_div(a.NQ * a.Hq, kCombineRows), (unsigned)a.B),
-                           dim3(64 * kCombineRows), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
+        hipLaunchKernelGGL(paged_attn_combine_kernel<D>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
+                           dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
                            a.NQ * a.Hq, a.max_blocks, partition, max_parts);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
@@ -659,7 +720,7 @@ int launch_valu(const Args &a) {
 
 int unsupported_rows(int gqa, int nq) {
     return dlmk::fail(DLMK_ERR_UNSUPPORTED,
-                      "dlmk_paged_decode_attention: no kernel for GQA group %d x %d queries", gqa, nq);
+                      "paged attention: no kernel for GQA group %d x %d queries", gqa, nq);
 }
 
 template <typename T, int D>
@@ -699,7 +760,7 @@ int dispatch_valu(const Args &a, int gqa) {
 
 int bad_dim(int head_dim, const char *dims) {
     return dlmk::fail(DLMK_ERR_UNSUPPORTED,
-                      "dlmk_paged_decode_attention: head_dim %d unsupported for this dtype (%s)",
+                      "paged attention: head_dim %d unsupported for this dtype (%s)",
                       head_dim, dims);
 }
 
@@ -721,32 +782,35 @@ size_t dlmk_paged_attention_workspace_size(int num_seqs, int num_q_per_seq, int 
     return (size_t)(o_aligned + rows * parts * 2 * 4);
 }
 
-int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const void *q,
-                                const void *k_pool, const void *v_pool, int dtype,
-                                const int32_t *block_tables, const int32_t *ctx_lens,
-                                int num_seqs, int num_q_per_seq, int num_q_heads,
-                                int num_kv_heads, int head_dim, int block_size,
-                                int max_blocks_per_seq, int64_t num_blocks, float scale,
-                                void *workspace, size_t workspace_bytes) {
+}  // extern "C"
+
+namespace {
+
+int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype, const void *q,
+                         void *k_pool, void *v_pool, int dtype, const void *k_new,
+                         const void *v_new, const int32_t *block_tables, const int32_t *ctx_lens,
+                         int num_seqs, int num_q_per_seq, int num_q_heads, int num_kv_heads,
+                         int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
+                         float scale, void *workspace, size_t workspace_bytes) {
     if (num_seqs < 0 || num_q_per_seq <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
         head_dim <= 0 || max_blocks_per_seq <= 0 || num_blocks < 0)
-        return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_paged_decode_attention: bad sizes");
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: bad sizes", who);
     if (num_q_heads % num_kv_heads != 0)
         return dlmk::fail(DLMK_ERR_INVALID_ARG,
-                          "dlmk_paged_decode_attention: %d query heads not a multiple of %d kv heads",
+                          "%s: %d query heads not a multiple of %d kv heads", who,
                           num_q_heads, num_kv_heads);
     if (num_seqs == 0) return DLMK_OK;
     if (!out || !q || !k_pool || !v_pool || !block_tables || !ctx_lens)
-        return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_paged_decode_attention: null pointer");
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: null pointer", who);
     if (block_size != kBlock)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED,
-                          "dlmk_paged_decode_attention: block_size %d unsupported (16)", block_size);
+                          "%s: block_size %d unsupported (16)", who, block_size);
     if (out_dtype != DLMK_F32 && out_dtype != DLMK_F16 && out_dtype != DLMK_BF16)
-        return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_paged_decode_attention: bad out dtype %d",
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: bad out dtype %d", who,
                           out_dtype);
     if ((int64_t)num_seqs * num_kv_heads > 0x7fffffff ||
         parts_for(max_blocks_per_seq, kMinPartition) > 65535 || num_seqs > 65535)
-        return dlmk::fail(DLMK_ERR_UNSUPPORTED, "dlmk_paged_decode_attention: grid too large");
+        return dlmk::fail(DLMK_ERR_UNSUPPORTED, "%s: grid too large", who);
 
     Args a;
     a.out = out;
@@ -754,6 +818,8 @@ int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const vo
     a.q = q;
     a.k_pool = k_pool;
     a.v_pool = v_pool;
+    a.k_new = k_new;
+    a.v_new = v_new;
     a.tables = block_tables;
     a.ctx_lens = ctx_lens;
     a.B = num_seqs;
@@ -772,11 +838,11 @@ int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const vo
             num_seqs, num_q_per_seq, num_q_heads, head_dim, block_size, max_blocks_per_seq);
         if (!workspace || workspace_bytes < need)
             return dlmk::fail(DLMK_ERR_WORKSPACE,
-                              "dlmk_paged_decode_attention: workspace %zu bytes, need %zu",
+                              "%s: workspace %zu bytes, need %zu", who,
                               workspace_bytes, need);
         if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
             return dlmk::fail(DLMK_ERR_INVALID_ARG,
-                              "dlmk_paged_decode_attention: workspace not 256-byte aligned");
+                              "%s: workspace not 256-byte aligned", who);
         const int64_t rows = (int64_t)num_seqs * num_q_per_seq * num_q_heads;
         a.workspace = workspace;
         a.ws_o_bytes = (rows * parts * head_dim * 4 + 255) / 256 * 256;
@@ -804,9 +870,42 @@ int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const vo
                 default: return bad_dim(head_dim, "64, 128, 256");
             }
         default:
-            return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_paged_decode_attention: bad KV dtype %d",
+            return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: bad KV dtype %d", who,
                               dtype);
     }
+}
+
+}  // namespace
+
+extern "C" {
+
+int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const void *q,
+                                const void *k_pool, const void *v_pool, int dtype,
+                                const int32_t *block_tables, const int32_t *ctx_lens,
+                                int num_seqs, int num_q_per_seq, int num_q_heads,
+                                int num_kv_heads, int head_dim, int block_size,
+                                int max_blocks_per_seq, int64_t num_blocks, float scale,
+                                void *workspace, size_t workspace_bytes) {
+    // Without new tokens the kernels never write the pools.
+    return paged_attention_impl("dlmk_paged_decode_attention", stream, out, out_dtype, q,
+                                const_cast<void *>(k_pool), const_cast<void *>(v_pool), dtype,
+                                nullptr, nullptr, block_tables, ctx_lens, num_seqs,
+                                num_q_per_seq, num_q_heads, num_kv_heads, head_dim, block_size,
+                                max_blocks_per_seq, num_blocks, scale, workspace, workspace_bytes);
+}
+
+int dlmk_paged_decode_step(void *stream, void *out, int out_dtype, const void *q, void *k_pool,
+                           void *v_pool, int dtype, const void *k_new, const void *v_new,
+                           const int32_t *block_tables, const int32_t *ctx_lens, int num_seqs,
+                           int num_q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
+                           int block_size, int max_blocks_per_seq, int64_t num_blocks, float scale,
+                           void *workspace, size_t workspace_bytes) {
+    if (num_seqs > 0 && (!k_new || !v_new))
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_paged_decode_step: null new-token pointer");
+    return paged_attention_impl("dlmk_paged_decode_step", stream, out, out_dtype, q, k_pool,
+                                v_pool, dtype, k_new, v_new, block_tables, ctx_lens, num_seqs,
+                                num_q_per_seq, num_q_heads, num_kv_heads, head_dim, block_size,
+                                max_blocks_per_seq, num_blocks, scale, workspace, workspace_bytes);
 }
 
 }  // extern "C"

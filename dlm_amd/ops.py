@@ -132,15 +132,8 @@ def alloc_workspace(nbytes: int, device="cuda") -> Optional[torch.Tensor]:
     return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
-def paged_decode_attention(q, k_pool, v_pool, block_tables, ctx_lens, *, num_kv_heads: int,
-                           scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
-                           out_dtype: Optional[torch.dtype] = None,
-                           workspace: Optional[torch.Tensor] = None,
-                           block_size: int = BLOCK_SIZE, stream=None) -> torch.Tensor:
-    """Paged GQA decode attention.
-
-    q: [B, nq, Hq, d] (nq > 1 is causal speculative verify); block_tables int32
-    [B, max_blocks]; ctx_lens int32 [B].  Returns out [B, nq, Hq, d]."""
+def _attention_call(q, k_pool, v_pool, block_tables, ctx_lens, num_kv_heads, scale, out,
+                    out_dtype, workspace, block_size, stream, k_new=None, v_new=None):
     _dev(q, "q")
     if q.dim() != 4:
         raise ValueError("q must be [num_seqs, num_q_per_seq, num_q_heads, head_dim]")
@@ -154,6 +147,13 @@ def paged_decode_attention(q, k_pool, v_pool, block_tables, ctx_lens, *, num_kv_
         raise TypeError("block_tables and ctx_lens must be int32")
     if block_tables.dim() != 2 or block_tables.shape[0] != B or ctx_lens.numel() != B:
         raise ValueError("block_tables must be [B, max_blocks] and ctx_lens [B]")
+    if k_new is not None:
+        for t, nm in ((k_new, "k_new"), (v_new, "v_new")):
+            _dev(t, nm)
+            if t.dtype != k_pool.dtype:
+                raise TypeError(f"{nm} dtype {t.dtype} != pool dtype {k_pool.dtype}")
+            if t.numel() != B * nq * num_kv_heads * d:
+                raise ValueError(f"{nm} must be [{B}, {nq}, {num_kv_heads}, {d}]")
     max_blocks = block_tables.shape[1]
     if scale is None:
         scale = 1.0 / math.sqrt(d)
@@ -167,12 +167,40 @@ def paged_decode_attention(q, k_pool, v_pool, block_tables, ctx_lens, *, num_kv_
         workspace = alloc_workspace(need, q.device)
     ws_ptr = workspace.data_ptr() if workspace is not None else None
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
-    check(lib().dlmk_paged_decode_attention(
-        _stream(stream), out.data_ptr(), dtype_code(out.dtype), q.data_ptr(), k_pool.data_ptr(),
-        v_pool.data_ptr(), dtype_code(q.dtype), block_tables.data_ptr(), ctx_lens.data_ptr(),
-        B, nq, Hq, num_kv_heads, d, block_size, max_blocks, num_blocks, float(scale), ws_ptr,
-        ws_bytes))
+    tail = (block_tables.data_ptr(), ctx_lens.data_ptr(), B, nq, Hq, num_kv_heads, d, block_size,
+            max_blocks, num_blocks, float(scale), ws_ptr, ws_bytes)
+    head = (_stream(stream), out.data_ptr(), dtype_code(out.dtype), q.data_ptr(),
+            k_pool.data_ptr(), v_pool.data_ptr(), dtype_code(q.dtype))
+    if k_new is None:
+        check(lib().dlmk_paged_decode_attention(*head, *tail))
+    else:
+        check(lib().dlmk_paged_decode_step(*head, k_new.data_ptr(), v_new.data_ptr(), *tail))
     return out
+
+
+def paged_decode_attention(q, k_pool, v_pool, block_tables, ctx_lens, *, num_kv_heads: int,
+                           scale: Optional[float] = None, out: Optional[torch.Tensor] = None,
+                           out_dtype: Optional[torch.dtype] = None,
+                           workspace: Optional[torch.Tensor] = None,
+                           block_size: int = BLOCK_SIZE, stream=None) -> torch.Tensor:
+    """Paged GQA decode attention.
+
+    q: [B, nq, Hq, d] (nq > 1 is causal speculative verify); block_tables int32
+    [B, max_blocks]; ctx_lens int32 [B].  Returns out [B, nq, Hq, d]."""
+    return _attention_call(q, k_pool, v_pool, block_tables, ctx_lens, num_kv_heads, scale, out,
+                           out_dtype, workspace, block_size, stream)
+
+
+def paged_decode_step(q, k_new, v_new, k_pool, v_pool, block_tables, ctx_lens, *,
+                      num_kv_heads: int, scale: Optional[float] = None,
+                      out: Optional[torch.Tensor] = None, out_dtype: Optional[torch.dtype] = None,
+                      workspace: Optional[torch.Tensor] = None, block_size: int = BLOCK_SIZE,
+                      stream=None) -> torch.Tensor:
+    """Fused decode step: append each sequence's nq newest tokens (k_new, v_new:
+    [B, nq, Hkv, d], at positions ctx - nq .. ctx - 1) and attend, in one launch.
+    Equivalent to kv_append followed by paged_decode_attention."""
+    return _attention_call(q, k_pool, v_pool, block_tables, ctx_lens, num_kv_heads, scale, out,
+                           out_dtype, workspace, block_size, stream, k_new, v_new)
 
 
 def _ids(t: torch.Tensor, name: str, cols: int) -> int:

@@ -188,6 +188,22 @@ int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const vo
                                 int max_blocks_per_seq, int64_t num_blocks, float scale,
                                 void *workspace, size_t workspace_bytes);
 
+/* Fused decode step: appends each sequence's num_q_per_seq newest tokens and
+ * runs dlmk_paged_decode_attention over them in one launch (the reference does
+ * the two back to back inside dlm_decode_block, kernels.cu:361-366).
+ * k_new / v_new are [num_seqs][num_q_per_seq][num_kv_heads][head_dim] in the
+ * pool dtype; token j of sequence s goes to position ctx_lens[s] -
+ * num_q_per_seq + j through block_tables (so ctx_lens already counts them and
+ * the table already holds their blocks, as PagedKvCache::append_tokens
+ * leaves it).  The pools receive exactly the bits dlmk_kv_append would write;
+ * out equals dlmk_kv_append followed by dlmk_paged_decode_attention. */
+int dlmk_paged_decode_step(void *stream, void *out, int out_dtype, const void *q, void *k_pool,
+                           void *v_pool, int dtype, const void *k_new, const void *v_new,
+                           const int32_t *block_tables, const int32_t *ctx_lens, int num_seqs,
+                           int num_q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
+                           int block_size, int max_blocks_per_seq, int64_t num_blocks, float scale,
+                           void *workspace, size_t workspace_bytes);
+
 /* Block copy for fork / copy-on-write: for each pairs[i] = (src, dst) (device
  * int32[n][2]) copy block src to block dst in both pools.  block_bytes is the
  * size of one block of one pool (num_kv_heads * block_size * head_dim * elem

@@ -48,3 +48,41 @@ def test_graph_replays_match_eager(cuda):
         g.replay()
         torch.cuda.synchronize()
         assert torch.equal(out, eager), f"replay {it} differs from eager"
+
+
+def test_graph_replays_fused_step(cuda):
+    """The fused decode step in a graph: each replay equals the eager call."""
+    import torch
+    from dlm_amd import ops
+    print("[gpu-test] graph replay of the fused decode step", flush=True)
+    rng = np.random.default_rng(41)
+    Hq, Hkv, d, nq = 32, 8, 128, 4
+    w = make_workload(rng, [900, 2500, 7], Hq, Hkv, d, np.float16, nq=nq, sigma=0.5)
+    kp, vp = to_dev(torch, w.k_pool, cuda), to_dev(torch, w.v_pool, cuda)
+    tables, lens = to_dev(torch, w.tables, cuda), to_dev(torch, w.ctx, cuda)
+    q = to_dev(torch, w.q, cuda)
+    knew = (torch.randn((3, nq, Hkv, d), device=cuda) * 0.5).half()
+    vnew = (torch.randn((3, nq, Hkv, d), device=cuda) * 0.5).half()
+    ws = ops.alloc_workspace(ops.attention_workspace_bytes(3, nq, Hq, d, w.tables.shape[1]), cuda)
+    out = torch.empty_like(q)
+
+    def step():
+        ops.paged_decode_step(q, knew, vnew, kp, vp, tables, lens, num_kv_heads=Hkv, out=out,
+                              workspace=ws)
+
+    step()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        step()
+    torch.cuda.synchronize()
+    for it in range(4):
+        knew.mul_(-1.0)
+        q.add_(0.125)
+        step()
+        torch.cuda.synchronize()
+        eager = out.clone()
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), f"replay {it} differs from eager"
