@@ -107,27 +107,39 @@ __device__ __forceinline__ int parts_of(int ctx, int P) { return ctx > P ? (ctx 
 
 // Shared epilogue: merge the NW waves' (m, l, O) of one work-group and either
 // finish the rows (single-partition sequence) or store the partition partial.
+// The ROWS x NW merge weights 2^(m_w - M) are computed once into LDS, so the
+// per-element pass is a plain weighted sum of the waves' O.
 template <int ROWS, int D, int NW, int GQA, int NQ>
 __device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][D],
                                             const float (&ml_lds)[NW][ROWS][2], void *out,
                                             int out_dtype, int seq, int kvh, int part,
                                             int nparts, int num_q_heads, int max_parts,
                                             float *ws_o, float *ws_ml) {
-    for (int idx = threadIdx.x; idx < ROWS * D; idx += NW * 64) {
-        const int r = idx / D, d = idx - r * D;
+    __shared__ float fac[ROWS][NW];
+    __shared__ float rowML[ROWS][2];
+    if (threadIdx.x < ROWS) {
+        const int r = threadIdx.x;
         float M = -INFINITY;
 #pragma unroll
         for (int w = 0; w < NW; ++w) M = fmaxf(M, ml_lds[w][r][0]);
-        float O = 0.f, L = 0.f;
-        if (M != -INFINITY) {
+        float L = 0.f;
 #pragma unroll
-            for (int w = 0; w < NW; ++w) {
-                const float mw = ml_lds[w][r][0];
-                const float f = mw == -INFINITY ? 0.f : exp2f(mw - M);
-                L = fmaf(f, ml_lds[w][r][1], L);
-                O = fmaf(f, o_lds[w][r][d], O);
-            }
+        for (int w = 0; w < NW; ++w) {
+            const float mw = ml_lds[w][r][0];
+            const float f = (M == -INFINITY || mw == -INFINITY) ? 0.f : exp2f(mw - M);
+            fac[r][w] = f;
+            L = fmaf(f, ml_lds[w][r][1], L);
         }
+        rowML[r][0] = M;
+        rowML[r][1] = L;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < ROWS * D; idx += NW * 64) {
+        const int r = idx / D, d = idx - r * D;
+        float O = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) O = fmaf(fac[r][w], o_lds[w][r][d], O);
+        const float L = rowML[r][1];
         const int j = r / GQA, h = kvh * GQA + r % GQA;
         const int64_t row = (int64_t)(seq * NQ + j) * num_q_heads + h;
         if (nparts == 1) {
@@ -136,7 +148,7 @@ __device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][D],
             const int64_t slot = row * max_parts + part;
             ws_o[slot * D + d] = O;
             if (d == 0) {
-                ws_ml[2 * slot] = M;
+                ws_ml[2 * slot] = rowML[r][0];
                 ws_ml[2 * slot + 1] = L;
             }
         }
