@@ -13,7 +13,7 @@ PKG = os.path.dirname(os.path.abspath(__file__))
 # DLMK_LIBRARY points at another build of the same ABI (e.g. a tuning variant).
 LIB_PATH = os.environ.get("DLMK_LIBRARY") or os.path.join(PKG, "libdlmk.so")
 
-DLMK_F32, DLMK_F16, DLMK_BF16 = 0, 1, 2
+DLMK_F32, DLMK_F16, DLMK_BF16, DLMK_I8, DLMK_I4 = 0, 1, 2, 3, 4
 DLMK_OK = 0
 DLMK_ERR_INVALID_ARG = -1
 DLMK_ERR_KV_EXHAUSTED = -2
@@ -72,6 +72,11 @@ SIGNATURES = {
                                            _sz]),
     "dlmk_paged_decode_step": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32,
                                       _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _vp, _sz]),
+    "dlmk_kv_append_quant": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i32,
+                                    _i32, _i32, _i64, _i32]),
+    "dlmk_paged_decode_attention_quant": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _vp, _vp, _i32,
+                                                 _vp, _vp, _i32, _i32, _i32, _i32, _i32, _i32,
+                                                 _i32, _i64, _f32, _vp, _sz]),
     "dlmk_copy_blocks": (_i32, [_vp, _vp, _vp, _vp, _i64, _sz, _i64]),
     "dlmk_gather_blocks": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _sz, _i64]),
     "dlmk_scatter_blocks": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _sz, _i64]),

@@ -192,6 +192,7 @@ struct Mfma;
 
 template <>
 struct Mfma<_Float16> {
+    using elem = _Float16;
     using x8 = f16x8;
     using x4 = f16x4;
     static __device__ __forceinline__ f32x4 qk(x8 a, x8 b, f32x4 c) {
@@ -204,6 +205,7 @@ struct Mfma<_Float16> {
 
 template <>
 struct Mfma<__bf16> {
+    using elem = __bf16;
     using x8 = bf16x8;
     using x4 = bf16x4;
     static __device__ __forceinline__ f32x4 qk(x8 a, x8 b, f32x4 c) {
@@ -216,27 +218,123 @@ struct Mfma<__bf16> {
     }
 };
 
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+// Storage codecs of the matrix-core kernel: where a lane's K chunk (8
+// consecutive dims of one token: the A operand of S^T = K.Q^T) and V piece (4
+// consecutive tokens of one dim: the B operand of O = P.V) sit in a (block,
+// kv head) tile, and how they widen to MFMA operands.  Quantized codecs keep
+// one f32 scale per token (K scales fold into the score, V scales multiply
+// the widened values); codes widen to f16 exactly (|code| <= 127).
+template <typename E>
+struct CodecFloat {  // f16 / bf16 pools: [d/8][16][8] and [d][16] elements
+    using QT = E;
+    using Op = Mfma<E>;
+    using KRaw = typename Op::x8;
+    using VRaw = typename Op::x4;
+    static constexpr bool kScaled = false;
+    static constexpr int kTileBytesPerDim = kBlock * sizeof(E);
+    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int i, int lane) {
+        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * i + lane);
+    }
+    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int g, int n) {
+        return stream_load(reinterpret_cast<const VRaw *>(tile) + ((16 * k + n) * kBlock + 4 * g) / 4);
+    }
+    static __device__ __forceinline__ typename Op::x8 k_op(KRaw r) { return r; }
+    static __device__ __forceinline__ typename Op::x4 v_op(VRaw r, f32x4, int, int g, int valid) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) r[e] = (4 * g + e < valid) ? r[e] : E(0.f);
+        return r;
+    }
+};
+
+struct CodecI8 {  // int8 pools: K [d/8][16][8] bytes, V [d][16] bytes
+    using QT = _Float16;
+    using Op = Mfma<_Float16>;
+    using KRaw = u32x2;
+    using VRaw = uint32_t;
+    static constexpr bool kScaled = true;
+    static constexpr int kTileBytesPerDim = kBlock;
+    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int i, int lane) {
+        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * i + lane);
+    }
+    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int g, int n) {
+        return stream_load(reinterpret_cast<const VRaw *>(tile + (16 * k + n) * kBlock + 4 * g));
+    }
+    static __device__ __forceinline__ f16x8 k_op(KRaw r) {
+        f16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (_Float16)(int8_t)(r[e / 4] >> (8 * (e % 4)));
+        return o;
+    }
+    static __device__ __forceinline__ f16x4 v_op(VRaw r, f32x4 vs, int, int g, int valid) {
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float v = (float)(int8_t)(r >> (8 * e)) * vs[e];
+            o[e] = (_Float16)(4 * g + e < valid ? v : 0.f);
+        }
+        return o;
+    }
+};
+
+struct CodecI4 {  // int4 pools: K [d/8][16][4] bytes, V [d/2][16] bytes (two dims per byte)
+    using QT = _Float16;
+    using Op = Mfma<_Float16>;
+    using KRaw = uint32_t;
+    using VRaw = uint32_t;
+    static constexpr bool kScaled = true;
+    static constexpr int kTileBytesPerDim = kBlock / 2;
+    static __device__ __forceinline__ int sext4(uint32_t nib) { return (int)(nib ^ 8u) - 8; }
+    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int i, int lane) {
+        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * i + lane);
+    }
+    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int g, int n) {
+        return stream_load(reinterpret_cast<const VRaw *>(tile + ((16 * k + n) >> 1) * kBlock + 4 * g));
+    }
+    static __device__ __forceinline__ f16x8 k_op(KRaw r) {
+        f16x8 o;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (_Float16)sext4((r >> (4 * e)) & 0xfu);
+        return o;
+    }
+    static __device__ __forceinline__ f16x4 v_op(VRaw r, f32x4 vs, int n, int g, int valid) {
+        f16x4 o;
+        const int sh = 4 * (n & 1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const float v = (float)sext4((r >> (8 * e + sh)) & 0xfu) * vs[e];
+            o[e] = (_Float16)(4 * g + e < valid ? v : 0.f);
+        }
+        return o;
+    }
+};
+
 #if DLMK_MFMA_WPE
 #define DLMK_MFMA_ATTRS __attribute__((amdgpu_waves_per_eu(DLMK_MFMA_WPE)))
 #else
 #define DLMK_MFMA_ATTRS
 #endif
 
-template <typename T, int D, int GQA, int NQ, int NW, int NB, int PD>
+template <typename C, int D, int GQA, int NQ, int NW, int NB, int PD>
 __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kernel(
-    void *__restrict__ out, int out_dtype, const T *__restrict__ q, T *__restrict__ k_pool,
-    T *__restrict__ v_pool, const T *__restrict__ k_new, const T *__restrict__ v_new,
+    void *__restrict__ out, int out_dtype, const typename C::QT *__restrict__ q,
+    uint8_t *__restrict__ k_pool, uint8_t *__restrict__ v_pool,
+    const float *__restrict__ k_scales, const float *__restrict__ v_scales,
+    const typename C::QT *__restrict__ k_new, const typename C::QT *__restrict__ v_new,
     const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
     int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
     int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
-    using M = Mfma<T>;
+    using M = typename C::Op;
     using x8 = typename M::x8;
     using x4 = typename M::x4;
+    using PT = typename M::elem;
+    using QT = typename C::QT;
     constexpr int ROWS = GQA * NQ;
-    constexpr int KI = D / 32;           // QK steps = 16-byte K loads per lane per block
-    constexpr int VN = D / 16;           // PV steps = 8-byte V loads per lane per block
+    constexpr int KI = D / 32;           // QK steps = K chunk loads per lane per block
+    constexpr int VN = D / 16;           // PV steps = V piece loads per lane per block
     constexpr int P = NW * NB * kBlock;  // tokens per work-group
-    constexpr int TILE = D * kBlock;     // elements per (block, kv head) tile
+    constexpr int64_t TILE = (int64_t)D * C::kTileBytesPerDim;  // bytes per (block, kv head)
     static_assert(ROWS <= 16 && D % 32 == 0, "unsupported geometry");
 
     __shared__ float o_lds[NW][ROWS][D];
@@ -295,14 +393,18 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
 #pragma unroll
     for (int k = 0; k < VN; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    if (k_new != nullptr) {
+    if constexpr (!C::kScaled) {
+        if (k_new != nullptr) {
 #pragma unroll
-        for (int b = 0; b < NB; ++b)
-            if (ok[b] && holds_new(lbs[b], ctx, NQ))
-                append_new_in_block<T, D>(k_pool, v_pool, k_new, v_new, blk[b], lbs[b], seq, kvh,
-                                          num_kv_heads, NQ, ctx, lane);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            for (int b = 0; b < NB; ++b)
+                if (ok[b] && holds_new(lbs[b], ctx, NQ))
+                    append_new_in_block<QT, D>(reinterpret_cast<QT *>(k_pool),
+                                               reinterpret_cast<QT *>(v_pool), k_new, v_new,
+                                               blk[b], lbs[b], seq, kvh, num_kv_heads, NQ, ctx,
+                                               lane);
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
     }
 
     if (nvalid > 0) {
@@ -318,18 +420,22 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         // blocks 0..NB-1, then V tiles): load stage t + PD is issued before
         // stage t is consumed, and scheduling barriers keep the compiler from
         // sinking the loads next to their uses.
-        x8 kb[NB][KI];
-        x4 vb[NB][VN];
+        typename C::KRaw kb[NB][KI];
+        typename C::VRaw vb[NB][VN];
+        f32x4 ksc[NB], vsc[NB];
         auto issue = [&](int t) {
             if (t < NB) {
-                const x8 *kp = reinterpret_cast<const x8 *>(k_pool + (blk[t] * num_kv_heads + kvh) * TILE);
+                const uint8_t *kt = k_pool + (blk[t] * num_kv_heads + kvh) * TILE;
 #pragma unroll
-                for (int i = 0; i < KI; ++i) kb[t][i] = stream_load(kp + 64 * i + lane);
+                for (int i = 0; i < KI; ++i) kb[t][i] = C::load_k(kt, i, lane);
+                if constexpr (C::kScaled)
+                    ksc[t] = *reinterpret_cast<const f32x4 *>(k_scales + blk[t] * kBlock + 4 * g);
             } else if (t < 2 * NB) {
-                const T *vt = v_pool + (blk[t - NB] * num_kv_heads + kvh) * TILE;
+                const uint8_t *vt = v_pool + (blk[t - NB] * num_kv_heads + kvh) * TILE;
 #pragma unroll
-                for (int k = 0; k < VN; ++k)
-                    vb[t - NB][k] = stream_load(reinterpret_cast<const x4 *>(vt + (16 * k + n) * kBlock + 4 * g));
+                for (int k = 0; k < VN; ++k) vb[t - NB][k] = C::load_v(vt, k, g, n);
+                if constexpr (C::kScaled)
+                    vsc[t - NB] = *reinterpret_cast<const f32x4 *>(v_scales + blk[t - NB] * kBlock + 4 * g);
             }
         };
 #pragma unroll
@@ -343,7 +449,8 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
             __builtin_amdgcn_sched_barrier(0);
             f32x4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < KI; ++i) c = M::qk(kb[b][i], qb[i], c);
+            for (int i = 0; i < KI; ++i) c = M::qk(C::k_op(kb[b][i]), qb[i], c);
+            if constexpr (C::kScaled) c *= ksc[b];
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int pos = lbs[b] * kBlock + 4 * g + j;
@@ -368,21 +475,17 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
             x4 pa;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const T ph = (T)(m == -INFINITY ? 0.f : exp2f(s[b][j] - m));
+                const PT ph = (PT)(m == -INFINITY ? 0.f : exp2f(s[b][j] - m));
                 pa[j] = ph;
                 lsum += (float)ph;
             }
             // Tokens past the context hold stale bytes (maybe NaN), and masked
-            // blocks hold another block's bytes: zero them so p = 0 contributes
-            // exactly nothing.
+            // blocks hold another block's bytes: v_op zeroes them so p = 0
+            // contributes exactly nothing.
             const int valid = ok[b] ? ctx - lbs[b] * kBlock : 0;
 #pragma unroll
-            for (int k = 0; k < VN; ++k) {
-                x4 vv = vb[b][k];
-#pragma unroll
-                for (int e = 0; e < 4; ++e) vv[e] = (4 * g + e < valid) ? vv[e] : T(0.f);
-                acc[k] = M::pv(pa, vv, acc[k]);
-            }
+            for (int k = 0; k < VN; ++k)
+                acc[k] = M::pv(pa, C::v_op(vb[b][k], vsc[b], n, g, valid), acc[k]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -671,7 +774,8 @@ struct Args {
     int out_dtype;
     const void *q;
     void *k_pool, *v_pool;
-    const void *k_new, *v_new;  // fused decode step: tokens appended in the same launch
+    const float *k_scales, *v_scales;  // quantized pools: one f32 per (block, token slot)
+    const void *k_new, *v_new;         // fused decode step: tokens appended in the same launch
     const int32_t *tables, *ctx_lens;
     int B, NQ, Hq, Hkv, max_blocks;
     int64_t num_blocks;
@@ -686,48 +790,54 @@ int64_t parts_for(int max_blocks, int partition) {
     return tokens > partition ? dlmk::ceil_div(tokens, partition) : 1;
 }
 
-template <typename T>
-using PartitionKernel = void (*)(void *, int, const T *, T *, T *, const T *, const T *,
-                                 const int32_t *, const int32_t *, int, int, int, int64_t, float,
-                                 int, float *, float *);
-
-template <typename T, int D>
-int launch_pair(const Args &a, PartitionKernel<T> kernel, int nw, int partition) {
+// Launches the partition kernel through `launch(grid, max_parts, ws_o, ws_ml)`,
+// then the combine kernel when a sequence can span several partitions.
+template <int D, typename Launch>
+int launch_pair(const Args &a, int partition, Launch launch) {
     const int max_parts = (int)parts_for(a.max_blocks, partition);
     float *ws_o = nullptr, *ws_ml = nullptr;
     if (max_parts > 1) {
         ws_o = static_cast<float *>(a.workspace);
         ws_ml = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + a.ws_o_bytes);
     }
-    dim3 grid((unsigned)(a.B * a.Hkv), (unsigned)max_parts);
-    hipLaunchKernelGGL(kernel, grid, dim3(nw * 64), 0, a.stream, a.out, a.out_dtype,
-                       static_cast<const T *>(a.q), static_cast<T *>(a.k_pool),
-                       static_cast<T *>(a.v_pool), static_cast<const T *>(a.k_new),
-                       static_cast<const T *>(a.v_new), a.tables, a.ctx_lens, a.Hq, a.Hkv,
-                       a.max_blocks, a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
+    launch(dim3((unsigned)(a.B * a.Hkv), (unsigned)max_parts), max_parts, ws_o, ws_ml);
     if (max_parts > 1)
         hipLaunchKernelGGL(paged_attn_combine_kernel<D>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
                            dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
                            a.NQ * a.Hq, a.max_blocks, partition, max_parts);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
-        return dlmk::fail((int)e, "dlmk_paged_decode_attention launch: %s", hipGetErrorString(e));
+        return dlmk::fail((int)e, "paged attention launch: %s", hipGetErrorString(e));
     return DLMK_OK;
 }
 
-// Matrix-core path: NW waves x NB blocks per partition.
-template <typename T, int D, int GQA, int NQ>
+// Matrix-core path: NW waves x NB blocks per partition, pool format C.
+template <typename C, int D, int GQA, int NQ>
 int launch_mfma(const Args &a) {
     constexpr int NW = DLMK_MFMA_NW, NB = DLMK_MFMA_NB, PD = DLMK_MFMA_PD;
     static_assert(NW * NB * kBlock >= kMinPartition, "partition below the workspace bound");
-    return launch_pair<T, D>(a, &paged_attn_mfma_kernel<T, D, GQA, NQ, NW, NB, PD>, NW,
-                             NW * NB * kBlock);
+    using QT = typename C::QT;
+    return launch_pair<D>(a, NW * NB * kBlock, [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
+        hipLaunchKernelGGL((paged_attn_mfma_kernel<C, D, GQA, NQ, NW, NB, PD>), grid, dim3(NW * 64), 0,
+                           a.stream, a.out, a.out_dtype, static_cast<const QT *>(a.q),
+                           static_cast<uint8_t *>(a.k_pool), static_cast<uint8_t *>(a.v_pool),
+                           a.k_scales, a.v_scales, static_cast<const QT *>(a.k_new),
+                           static_cast<const QT *>(a.v_new), a.tables, a.ctx_lens, a.Hq, a.Hkv,
+                           a.max_blocks, a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
+    });
 }
 
 template <int D, int GQA, int NQ>
 int launch_valu(const Args &a) {
     constexpr int NW = GQA * NQ <= 4 ? 4 : 8;
-    return launch_pair<float, D>(a, &paged_attn_valu_kernel<D, GQA, NQ, NW>, NW, kMinPartition);
+    return launch_pair<D>(a, kMinPartition, [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
+        hipLaunchKernelGGL((paged_attn_valu_kernel<D, GQA, NQ, NW>), grid, dim3(NW * 64), 0, a.stream,
+                           a.out, a.out_dtype, static_cast<const float *>(a.q),
+                           static_cast<float *>(a.k_pool), static_cast<float *>(a.v_pool),
+                           static_cast<const float *>(a.k_new), static_cast<const float *>(a.v_new),
+                           a.tables, a.ctx_lens, a.Hq, a.Hkv, a.max_blocks, a.num_blocks,
+                           a.scale * kLog2e, max_parts, ws_o, ws_ml);
+    });
 }
 
 int unsupported_rows(int gqa, int nq) {
@@ -735,21 +845,21 @@ int unsupported_rows(int gqa, int nq) {
                       "paged attention: no kernel for GQA group %d x %d queries", gqa, nq);
 }
 
-template <typename T, int D>
+template <typename C, int D>
 int dispatch_mfma(const Args &a, int gqa) {
     switch (gqa * 16 + a.NQ) {
-        case 1 * 16 + 1: return launch_mfma<T, D, 1, 1>(a);
-        case 1 * 16 + 2: return launch_mfma<T, D, 1, 2>(a);
-        case 1 * 16 + 4: return launch_mfma<T, D, 1, 4>(a);
-        case 2 * 16 + 1: return launch_mfma<T, D, 2, 1>(a);
-        case 2 * 16 + 2: return launch_mfma<T, D, 2, 2>(a);
-        case 2 * 16 + 4: return launch_mfma<T, D, 2, 4>(a);
-        case 4 * 16 + 1: return launch_mfma<T, D, 4, 1>(a);
-        case 4 * 16 + 2: return launch_mfma<T, D, 4, 2>(a);
-        case 4 * 16 + 4: return launch_mfma<T, D, 4, 4>(a);
-        case 8 * 16 + 1: return launch_mfma<T, D, 8, 1>(a);
-        case 8 * 16 + 2: return launch_mfma<T, D, 8, 2>(a);
-        case 16 * 16 + 1: return launch_mfma<T, D, 16, 1>(a);
+        case 1 * 16 + 1: return launch_mfma<C, D, 1, 1>(a);
+        case 1 * 16 + 2: return launch_mfma<C, D, 1, 2>(a);
+        case 1 * 16 + 4: return launch_mfma<C, D, 1, 4>(a);
+        case 2 * 16 + 1: return launch_mfma<C, D, 2, 1>(a);
+        case 2 * 16 + 2: return launch_mfma<C, D, 2, 2>(a);
+        case 2 * 16 + 4: return launch_mfma<C, D, 2, 4>(a);
+        case 4 * 16 + 1: return launch_mfma<C, D, 4, 1>(a);
+        case 4 * 16 + 2: return launch_mfma<C, D, 4, 2>(a);
+        case 4 * 16 + 4: return launch_mfma<C, D, 4, 4>(a);
+        case 8 * 16 + 1: return launch_mfma<C, D, 8, 1>(a);
+        case 8 * 16 + 2: return launch_mfma<C, D, 8, 2>(a);
+        case 16 * 16 + 1: return launch_mfma<C, D, 16, 1>(a);
         default: return unsupported_rows(gqa, a.NQ);
     }
 }
@@ -799,7 +909,8 @@ size_t dlmk_paged_attention_workspace_size(int num_seqs, int num_q_per_seq, int 
 namespace {
 
 int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype, const void *q,
-                         void *k_pool, void *v_pool, int dtype, const void *k_new,
+                         void *k_pool, void *v_pool, int dtype, const float *k_scales,
+                         const float *v_scales, const void *k_new,
                          const void *v_new, const int32_t *block_tables, const int32_t *ctx_lens,
                          int num_seqs, int num_q_per_seq, int num_q_heads, int num_kv_heads,
                          int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
@@ -814,6 +925,11 @@ int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype
     if (num_seqs == 0) return DLMK_OK;
     if (!out || !q || !k_pool || !v_pool || !block_tables || !ctx_lens)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: null pointer", who);
+    const bool quant = dtype == DLMK_I8 || dtype == DLMK_I4;
+    if (quant && (!k_scales || !v_scales))
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: null scale pointer", who);
+    if (quant && k_new)
+        return dlmk::fail(DLMK_ERR_UNSUPPORTED, "%s: no fused append into quantized pools", who);
     if (block_size != kBlock)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED,
                           "%s: block_size %d unsupported (16)", who, block_size);
@@ -830,6 +946,8 @@ int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype
     a.q = q;
     a.k_pool = k_pool;
     a.v_pool = v_pool;
+    a.k_scales = k_scales;
+    a.v_scales = v_scales;
     a.k_new = k_new;
     a.v_new = v_new;
     a.tables = block_tables;
@@ -869,16 +987,30 @@ int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype
             }
         case DLMK_F16:
             switch (head_dim) {
-                case 64: return dispatch_mfma<_Float16, 64>(a, gqa);
-                case 128: return dispatch_mfma<_Float16, 128>(a, gqa);
-                case 256: return dispatch_mfma<_Float16, 256>(a, gqa);
+                case 64: return dispatch_mfma<CodecFloat<_Float16>, 64>(a, gqa);
+                case 128: return dispatch_mfma<CodecFloat<_Float16>, 128>(a, gqa);
+                case 256: return dispatch_mfma<CodecFloat<_Float16>, 256>(a, gqa);
                 default: return bad_dim(head_dim, "64, 128, 256");
             }
         case DLMK_BF16:
             switch (head_dim) {
-                case 64: return dispatch_mfma<__bf16, 64>(a, gqa);
-                case 128: return dispatch_mfma<__bf16, 128>(a, gqa);
-                case 256: return dispatch_mfma<__bf16, 256>(a, gqa);
+                case 64: return dispatch_mfma<CodecFloat<__bf16>, 64>(a, gqa);
+                case 128: return dispatch_mfma<CodecFloat<__bf16>, 128>(a, gqa);
+                case 256: return dispatch_mfma<CodecFloat<__bf16>, 256>(a, gqa);
+                default: return bad_dim(head_dim, "64, 128, 256");
+            }
+        case DLMK_I8:
+            switch (head_dim) {
+                case 64: return dispatch_mfma<CodecI8, 64>(a, gqa);
+                case 128: return dispatch_mfma<CodecI8, 128>(a, gqa);
+                case 256: return dispatch_mfma<CodecI8, 256>(a, gqa);
+                default: return bad_dim(head_dim, "64, 128, 256");
+            }
+        case DLMK_I4:
+            switch (head_dim) {
+                case 64: return dispatch_mfma<CodecI4, 64>(a, gqa);
+                case 128: return dispatch_mfma<CodecI4, 128>(a, gqa);
+                case 256: return dispatch_mfma<CodecI4, 256>(a, gqa);
                 default: return bad_dim(head_dim, "64, 128, 256");
             }
         default:
@@ -901,7 +1033,7 @@ int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const vo
     // Without new tokens the kernels never write the pools.
     return paged_attention_impl("dlmk_paged_decode_attention", stream, out, out_dtype, q,
                                 const_cast<void *>(k_pool), const_cast<void *>(v_pool), dtype,
-                                nullptr, nullptr, block_tables, ctx_lens, num_seqs,
+                                nullptr, nullptr, nullptr, nullptr, block_tables, ctx_lens, num_seqs,
                                 num_q_per_seq, num_q_heads, num_kv_heads, head_dim, block_size,
                                 max_blocks_per_seq, num_blocks, scale, workspace, workspace_bytes);
 }
@@ -915,9 +1047,32 @@ int dlmk_paged_decode_step(void *stream, void *out, int out_dtype, const void *q
     if (num_seqs > 0 && (!k_new || !v_new))
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_paged_decode_step: null new-token pointer");
     return paged_attention_impl("dlmk_paged_decode_step", stream, out, out_dtype, q, k_pool,
-                                v_pool, dtype, k_new, v_new, block_tables, ctx_lens, num_seqs,
+                                v_pool, dtype, nullptr, nullptr, k_new, v_new, block_tables, ctx_lens, num_seqs,
                                 num_q_per_seq, num_q_heads, num_kv_heads, head_dim, block_size,
                                 max_blocks_per_seq, num_blocks, scale, workspace, workspace_bytes);
+}
+
+}  // extern "C"
+
+extern "C" {
+
+int dlmk_paged_decode_attention_quant(void *stream, void *out, int out_dtype, const void *q,
+                                      const void *k_pool, const void *v_pool,
+                                      const float *k_scales, const float *v_scales, int quant,
+                                      const int32_t *block_tables, const int32_t *ctx_lens,
+                                      int num_seqs, int num_q_per_seq, int num_q_heads,
+                                      int num_kv_heads, int head_dim, int block_size,
+                                      int max_blocks_per_seq, int64_t num_blocks, float scale,
+                                      void *workspace, size_t workspace_bytes) {
+    if (quant != DLMK_I8 && quant != DLMK_I4)
+        return dlmk::fail(DLMK_ERR_INVALID_ARG,
+                          "dlmk_paged_decode_attention_quant: bad quant %d", quant);
+    return paged_attention_impl("dlmk_paged_decode_attention_quant", stream, out, out_dtype, q,
+                                const_cast<void *>(k_pool), const_cast<void *>(v_pool), quant,
+                                k_scales, v_scales, nullptr, nullptr, block_tables, ctx_lens,
+                                num_seqs, num_q_per_seq, num_q_heads, num_kv_heads, head_dim,
+                                block_size, max_blocks_per_seq, num_blocks, scale, workspace,
+                                workspace_bytes);
 }
 
 }  // extern "C"

@@ -15,7 +15,7 @@ from typing import Optional
 
 import torch
 
-from ._lib import DLMK_BF16, DLMK_F16, DLMK_F32, check, lib
+from ._lib import DLMK_BF16, DLMK_F16, DLMK_F32, DLMK_I4, DLMK_I8, check, lib
 
 BLOCK_SIZE = 16  # tokens per block; dlm hard-codes 16 (src/main.rs:455, src/loader.rs:597)
 
@@ -133,14 +133,20 @@ def alloc_workspace(nbytes: int, device="cuda") -> Optional[torch.Tensor]:
 
 
 def _attention_call(q, k_pool, v_pool, block_tables, ctx_lens, num_kv_heads, scale, out,
-                    out_dtype, workspace, block_size, stream, k_new=None, v_new=None):
+                    out_dtype, workspace, block_size, stream, k_new=None, v_new=None,
+                    quant: Optional["QuantKv"] = None):
     _dev(q, "q")
     if q.dim() != 4:
         raise ValueError("q must be [num_seqs, num_q_per_seq, num_q_heads, head_dim]")
     B, nq, Hq, d = q.shape
-    num_blocks = _pool_geom(k_pool, v_pool, num_kv_heads, d, block_size)
-    if q.dtype != k_pool.dtype:
-        raise TypeError(f"q dtype {q.dtype} != pool dtype {k_pool.dtype}")
+    if quant is None:
+        num_blocks = _pool_geom(k_pool, v_pool, num_kv_heads, d, block_size)
+        if q.dtype != k_pool.dtype:
+            raise TypeError(f"q dtype {q.dtype} != pool dtype {k_pool.dtype}")
+    else:
+        num_blocks = quant.check(num_kv_heads, d, block_size)
+        if q.dtype != torch.float16:
+            raise TypeError(f"q must be float16 for quantized pools (got {q.dtype})")
     _dev(block_tables, "block_tables")
     _dev(ctx_lens, "ctx_lens")
     if block_tables.dtype != torch.int32 or ctx_lens.dtype != torch.int32:
@@ -169,6 +175,12 @@ def _attention_call(q, k_pool, v_pool, block_tables, ctx_lens, num_kv_heads, sca
     ws_bytes = workspace.numel() * workspace.element_size() if workspace is not None else 0
     tail = (block_tables.data_ptr(), ctx_lens.data_ptr(), B, nq, Hq, num_kv_heads, d, block_size,
             max_blocks, num_blocks, float(scale), ws_ptr, ws_bytes)
+    if quant is not None:
+        check(lib().dlmk_paged_decode_attention_quant(
+            _stream(stream), out.data_ptr(), dtype_code(out.dtype), q.data_ptr(),
+            quant.k.data_ptr(), quant.v.data_ptr(), quant.k_scales.data_ptr(),
+            quant.v_scales.data_ptr(), quant.code, *tail))
+        return out
     head = (_stream(stream), out.data_ptr(), dtype_code(out.dtype), q.data_ptr(),
             k_pool.data_ptr(), v_pool.data_ptr(), dtype_code(q.dtype))
     if k_new is None:
@@ -201,6 +213,118 @@ def paged_decode_step(q, k_new, v_new, k_pool, v_pool, block_tables, ctx_lens, *
     Equivalent to kv_append followed by paged_decode_attention."""
     return _attention_call(q, k_pool, v_pool, block_tables, ctx_lens, num_kv_heads, scale, out,
                            out_dtype, workspace, block_size, stream, k_new, v_new)
+
+
+_QUANT = {"int8": (DLMK_I8, 8), "int4": (DLMK_I4, 4)}
+
+
+@dataclass(frozen=True)
+class QuantKv:
+    """One layer's quantized KV pools (dlm's --kv-quant int8 / int4).
+
+    k, v: uint8 code pools; k_scales, v_scales: float32 [num_blocks, block_size],
+    one scale per token slot over the whole kv_dim."""
+
+    k: torch.Tensor
+    v: torch.Tensor
+    k_scales: torch.Tensor
+    v_scales: torch.Tensor
+    quant: str
+
+    @property
+    def code(self) -> int:
+        return _QUANT[self.quant][0]
+
+    @property
+    def bits(self) -> int:
+        return _QUANT[self.quant][1]
+
+    @property
+    def num_blocks(self) -> int:
+        return self.k_scales.shape[0]
+
+    def block_bytes(self) -> int:
+        """Bytes of one block of one code pool."""
+        return self.k.numel() // self.num_blocks
+
+    def check(self, num_kv_heads: int, head_dim: int, block_size: int) -> int:
+        """Validate against (Hkv, d, block_size); return num_blocks."""
+        if self.quant not in _QUANT:
+            raise ValueError(f"quant must be int8 or int4 (got {self.quant!r})")
+        for t, nm in ((self.k, "k"), (self.v, "v"), (self.k_scales, "k_scales"),
+                      (self.v_scales, "v_scales")):
+            _dev(t, nm)
+        if self.k.dtype != torch.uint8 or self.v.dtype != torch.uint8:
+            raise TypeError("quantized code pools must be uint8")
+        if self.k_scales.dtype != torch.float32 or self.v_scales.dtype != torch.float32:
+            raise TypeError("scales must be float32")
+        nb = self.num_blocks
+        if self.k_scales.shape != (nb, block_size) or self.v_scales.shape != (nb, block_size):
+            raise ValueError("scales must be [num_blocks, block_size]")
+        per_block = num_kv_heads * head_dim * block_size * self.bits // 8
+        if self.k.numel() != nb * per_block or self.v.numel() != nb * per_block:
+            raise ValueError(f"code pools must hold {nb} blocks of {per_block} bytes")
+        return nb
+
+
+def alloc_quant_pools(num_blocks: int, num_kv_heads: int, head_dim: int, quant: str,
+                      device="cuda", block_size: int = BLOCK_SIZE) -> QuantKv:
+    """Allocate one layer's int8 / int4 pools in the library's layout:
+    int8 K [nb, Hkv, d/8, 16, 8], V [nb, Hkv, d, 16]; int4 K [nb, Hkv, d/8, 16, 4],
+    V [nb, Hkv, d/2, 16]; scales [nb, 16] float32 (zero)."""
+    if quant not in _QUANT:
+        raise ValueError(f"quant must be int8 or int4 (got {quant!r})")
+    if head_dim % 8 != 0:
+        raise ValueError("head_dim must be a multiple of 8")
+    nb, H, d, bs = num_blocks, num_kv_heads, head_dim, block_size
+    if quant == "int8":
+        ks, vs = (nb, H, d // 8, bs, 8), (nb, H, d, bs)
+    else:
+        ks, vs = (nb, H, d // 8, bs, 4), (nb, H, d // 2, bs)
+    return QuantKv(torch.zeros(ks, dtype=torch.uint8, device=device),
+                   torch.zeros(vs, dtype=torch.uint8, device=device),
+                   torch.zeros((nb, bs), dtype=torch.float32, device=device),
+                   torch.zeros((nb, bs), dtype=torch.float32, device=device), quant)
+
+
+def kv_append_quant(kv: QuantKv, k, v, slot_mapping, *, num_kv_heads: int, head_dim: int,
+                    block_size: int = BLOCK_SIZE, stream=None) -> None:
+    """Quantize tokens k, v ([n, Hkv, d], f32/f16/bf16) per token and scatter
+    codes and scales into their slots (KvLayerCache::append's int8/int4 branch)."""
+    nb = kv.check(num_kv_heads, head_dim, block_size)
+    for t, nm in ((k, "k"), (v, "v")):
+        _dev(t, nm)
+    if k.dtype != v.dtype:
+        raise TypeError("k and v must share a dtype")
+    _dev(slot_mapping, "slot_mapping")
+    if slot_mapping.dtype != torch.int64:
+        raise TypeError("slot_mapping must be int64")
+    n = slot_mapping.numel()
+    if k.numel() != n * num_kv_heads * head_dim or v.numel() != k.numel():
+        raise ValueError(f"k/v hold {k.numel()}/{v.numel()} elements, expected "
+                         f"{n}x{num_kv_heads}x{head_dim}")
+    check(lib().dlmk_kv_append_quant(_stream(stream), kv.k.data_ptr(), kv.v.data_ptr(),
+                                     kv.k_scales.data_ptr(), kv.v_scales.data_ptr(),
+                                     k.data_ptr(), v.data_ptr(), dtype_code(k.dtype),
+                                     slot_mapping.data_ptr(), n, num_kv_heads, head_dim,
+                                     block_size, nb, kv.code))
+
+
+def paged_decode_attention_quant(q, kv: QuantKv, block_tables, ctx_lens, *, num_kv_heads: int,
+                                 scale: Optional[float] = None,
+                                 out: Optional[torch.Tensor] = None,
+                                 out_dtype: Optional[torch.dtype] = None,
+                                 workspace: Optional[torch.Tensor] = None,
+                                 block_size: int = BLOCK_SIZE, stream=None) -> torch.Tensor:
+    """Paged GQA decode attention over int8 / int4 pools; q float16 [B, nq, Hq, d]."""
+    return _attention_call(q, None, None, block_tables, ctx_lens, num_kv_heads, scale, out,
+                           out_dtype, workspace, block_size, stream, quant=kv)
+
+
+def copy_blocks_quant(kv: QuantKv, pairs, stream=None) -> None:
+    """Fork / copy-on-write for quantized pools: codes and scales of each pair."""
+    copy_blocks(kv.k, kv.v, pairs, kv.block_bytes(), stream)
+    copy_blocks(kv.k_scales, kv.v_scales, pairs, kv.k_scales.shape[1] * 4, stream)
 
 
 def _ids(t: torch.Tensor, name: str, cols: int) -> int:

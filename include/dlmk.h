@@ -40,8 +40,9 @@ extern "C" {
 
 #define DLMK_ABI_VERSION 1
 
-/* Element types of K/V pools, queries and outputs. */
-enum dlmk_dtype { DLMK_F32 = 0, DLMK_F16 = 1, DLMK_BF16 = 2 };
+/* Element types of K/V pools, queries and outputs; DLMK_I8 / DLMK_I4 are the
+ * quantized pool formats (dlm's KvQuant::Int8 / Int4, src/forward/cpu.rs:627-639). */
+enum dlmk_dtype { DLMK_F32 = 0, DLMK_F16 = 1, DLMK_BF16 = 2, DLMK_I8 = 3, DLMK_I4 = 4 };
 
 /* Negative status codes (positive values are hipError_t). */
 #define DLMK_OK 0
@@ -203,6 +204,41 @@ int dlmk_paged_decode_step(void *stream, void *out, int out_dtype, const void *q
                            int num_q_per_seq, int num_q_heads, int num_kv_heads, int head_dim,
                            int block_size, int max_blocks_per_seq, int64_t num_blocks, float scale,
                            void *workspace, size_t workspace_bytes);
+
+/* Quantized KV pools (dlm's --kv-quant int8 / int4, KvLayerCache at
+ * src/forward/cpu.rs:622-711).  Each token carries one f32 scale per pool over
+ * its whole kv_dim (num_kv_heads * head_dim values): scale = max|x| / qmax
+ * (qmax 127 / 7), code = round-half-away(x / scale) clamped to +-qmax, and an
+ * all-zero token has scale 0 and zero codes.  Layouts per layer (block_size 16):
+ *   int8: K [num_blocks][Hkv][d/8][16][8] bytes, V [num_blocks][Hkv][d][16] bytes
+ *   int4: K [num_blocks][Hkv][d/8][16][4] bytes (two elements a byte, low
+ *         nibble the even one), V [num_blocks][Hkv][d/2][16] bytes (dims 2p and
+ *         2p+1 of one token in one byte, low nibble 2p)
+ *   scales: k_scales / v_scales f32 [num_blocks][16] (slot order).
+ * Append: replaces KvLayerCache::append's quantizing branch (cpu.rs:765-795,
+ * quantize_i8 / quantize_i4 at :672-711).  k_src / v_src are
+ * [n_tok][num_kv_heads][head_dim] in src_dtype (f32, f16, bf16); token i goes
+ * to slot_mapping[i]; negative or out-of-pool slots are skipped.  quant is
+ * DLMK_I8 or DLMK_I4; head_dim a multiple of 8. */
+int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, float *k_scales,
+                         float *v_scales, const void *k_src, const void *v_src, int src_dtype,
+                         const int64_t *slot_mapping, int64_t n_tok, int num_kv_heads,
+                         int head_dim, int block_size, int64_t num_blocks, int quant);
+
+/* Paged decode attention over quantized pools: replaces attention() with
+ * key_head_dot / value_head_accumulate's dequantizing branches
+ * (cpu.rs:798-846, :1126-1151).  q is f16; every other argument, the
+ * causal rule, masking and the workspace are as in dlmk_paged_decode_attention
+ * (the same workspace size function applies).  Scores are
+ * dot(q, k_code) * k_scale * scale; values are v_code * v_scale. */
+int dlmk_paged_decode_attention_quant(void *stream, void *out, int out_dtype, const void *q,
+                                      const void *k_pool, const void *v_pool,
+                                      const float *k_scales, const float *v_scales, int quant,
+                                      const int32_t *block_tables, const int32_t *ctx_lens,
+                                      int num_seqs, int num_q_per_seq, int num_q_heads,
+                                      int num_kv_heads, int head_dim, int block_size,
+                                      int max_blocks_per_seq, int64_t num_blocks, float scale,
+                                      void *workspace, size_t workspace_bytes);
 
 /* Block copy for fork / copy-on-write: for each pairs[i] = (src, dst) (device
  * int32[n][2]) copy block src to block dst in both pools.  block_bytes is the

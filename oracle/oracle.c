@@ -548,3 +548,189 @@ float orc_read_i4(const uint8_t *packed, int64_t base, int64_t i) {
     int code = nib >= 8 ? (int)nib - 16 : (int)nib;
     return (float)code;
 }
+
+/* ------------------------------------------------------------------------ */
+/* Quantized KV store (KvStore::Int8 / Int4, src/forward/cpu.rs:641-661) and */
+/* its attention (key_head_dot / value_head_accumulate, :798-846).           */
+/* Contiguous reference layout: int8 codes [pos][kv_dim]; int4 codes packed  */
+/* [pos][ceil(kv_dim/2)] (element i in byte i/2, low nibble for even i);     */
+/* one f32 scale per position for K and one for V.                           */
+/* ------------------------------------------------------------------------ */
+
+#define ORC_I8 3
+#define ORC_I4 4
+
+static float quant_code(const void *codes, int64_t row_base, int64_t i, int quant) {
+    if (quant == ORC_I8) return (float)((const int8_t *)codes)[row_base + i];
+    return orc_read_i4((const uint8_t *)codes, row_base, i);
+}
+
+static int64_t quant_row_bytes(int64_t kv_dim, int quant) {
+    return quant == ORC_I8 ? kv_dim : (kv_dim + 1) / 2;
+}
+
+/* attention() over a quantized history: a * (code * s) per key element
+ * (:808-818) and o += w * (code * s) per value element (:833-845). */
+void orc_attention_quant(const float *q, const void *kcodes, const float *kscales,
+                         const void *vcodes, const float *vscales, int64_t positions,
+                         int num_heads, int num_kv_heads, int head_dim, float scale, int quant,
+                         float *ctx) {
+    int d = head_dim, group = num_heads / num_kv_heads;
+    int64_t kv_dim = (int64_t)num_kv_heads * d, rb = quant_row_bytes(kv_dim, quant);
+    float *scores = (float *)malloc(sizeof(float) * (positions ? positions : 1));
+    for (int h = 0; h < num_heads; ++h) {
+        int kvh = h / group;
+        const float *qh = q + (int64_t)h * d;
+        for (int64_t p = 0; p < positions; ++p) {
+            float s = kscales[p], dot = 0.0f;
+            for (int j = 0; j < d; ++j)
+                dot += qh[j] * (quant_code(kcodes, p * rb, (int64_t)kvh * d + j, quant) * s);
+            scores[p] = dot * scale;
+        }
+        softmax_inplace(scores, positions);
+        float *out = ctx + (int64_t)h * d;
+        for (int j = 0; j < d; ++j) out[j] = 0.0f;
+        for (int64_t p = 0; p < positions; ++p) {
+            float s = vscales[p], w = scores[p];
+            for (int j = 0; j < d; ++j)
+                out[j] += w * (quant_code(vcodes, p * rb, (int64_t)kvh * d + j, quant) * s);
+        }
+    }
+    free(scores);
+}
+
+/* KvLayerCache::append for the quantized stores (:780-793): quantize each
+ * token's K and V over the whole kv_dim; codes go to the contiguous layout. */
+void orc_quantize_tokens(const float *src, int64_t n_tok, int64_t kv_dim, int quant, void *codes,
+                         float *scales) {
+    int64_t rb = quant_row_bytes(kv_dim, quant);
+    for (int64_t i = 0; i < n_tok; ++i) {
+        if (quant == ORC_I8)
+            scales[i] = orc_quantize_i8(src + i * kv_dim, kv_dim, (int8_t *)codes + i * rb);
+        else
+            scales[i] = orc_quantize_i4(src + i * kv_dim, kv_dim, (uint8_t *)codes + i * rb);
+    }
+}
+
+/* Paged quantized pools (layout of this build, no reference counterpart):
+ *   K codes: int8 [nb][Hkv][d/8][16][8] bytes; int4 [nb][Hkv][d/8][16][4]
+ *            (8 consecutive dims per chunk, element e in byte e/2, low nibble
+ *            for even e)
+ *   V codes: int8 [nb][Hkv][d][16] bytes;     int4 [nb][Hkv][d/2][16]
+ *            (byte (p, t) = dims 2p and 2p+1 of token t, low nibble for the
+ *            even dim: a byte never mixes tokens, so appends never share one)
+ *   scales:  K and V f32 [nb][16], one per token (shared by all heads). */
+static void put_nibble(uint8_t *b, int hi, int code) {
+    uint8_t nib = (uint8_t)code & 0x0f;
+    *b = hi ? (uint8_t)((*b & 0x0f) | (nib << 4)) : (uint8_t)((*b & 0xf0) | nib);
+}
+static int get_nibble(const uint8_t *b, int hi) {
+    int nib = hi ? (*b >> 4) : (*b & 0x0f);
+    return nib >= 8 ? nib - 16 : nib;
+}
+
+static int64_t qk_off(int64_t blk, int h, int t, int j, int Hkv, int d, int quant) {
+    int64_t tile = (blk * Hkv + h) * (int64_t)d * 16;  /* elements */
+    int64_t el = tile + ((int64_t)(j / 8) * 16 + t) * 8 + (j % 8);
+    return quant == ORC_I8 ? el : el / 2; /* byte offset (int4: nibble el % 2) */
+}
+static int64_t qv_off(int64_t blk, int h, int t, int j, int Hkv, int d, int quant) {
+    if (quant == ORC_I8) return (blk * Hkv + h) * (int64_t)d * 16 + (int64_t)j * 16 + t;
+    return ((blk * Hkv + h) * (int64_t)(d / 2) + j / 2) * 16 + t; /* nibble j % 2 */
+}
+
+/* Quantize n_tok tokens (src [n][Hkv][d] f32) and scatter codes + scales. */
+void orc_paged_append_quant(void *k_pool, void *v_pool, float *k_scales, float *v_scales,
+                            const float *k_src, const float *v_src, const int64_t *slots,
+                            int64_t n_tok, int Hkv, int d, int bs, int quant, int64_t num_blocks) {
+    int64_t kv_dim = (int64_t)Hkv * d, rb = quant_row_bytes(kv_dim, quant);
+    void *kc = malloc(rb), *vc = malloc(rb);
+    for (int64_t i = 0; i < n_tok; ++i) {
+        int64_t slot = slots[i];
+        if (slot < 0 || slot >= num_blocks * bs) continue;
+        int64_t blk = slot / bs;
+        int t = (int)(slot % bs);
+        float ks, vs;
+        orc_quantize_tokens(k_src + i * kv_dim, 1, kv_dim, quant, kc, &ks);
+        orc_quantize_tokens(v_src + i * kv_dim, 1, kv_dim, quant, vc, &vs);
+        k_scales[slot] = ks;
+        v_scales[slot] = vs;
+        for (int h = 0; h < Hkv; ++h)
+            for (int j = 0; j < d; ++j) {
+                int e = h * d + j;
+                int kq = (int)quant_code(kc, 0, e, quant), vq = (int)quant_code(vc, 0, e, quant);
+                int64_t ko = qk_off(blk, h, t, j, Hkv, d, quant);
+                int64_t vo = qv_off(blk, h, t, j, Hkv, d, quant);
+                if (quant == ORC_I8) {
+                    ((int8_t *)k_pool)[ko] = (int8_t)kq;
+                    ((int8_t *)v_pool)[vo] = (int8_t)vq;
+                } else {
+                    put_nibble((uint8_t *)k_pool + ko, (j % 8) % 2, kq);
+                    put_nibble((uint8_t *)v_pool + vo, j % 2, vq);
+                }
+            }
+    }
+    free(kc);
+    free(vc);
+}
+
+/* Logical view of a paged quantized sequence in the reference's contiguous
+ * layout (codes + per-position scales). */
+void orc_paged_gather_quant(const void *k_pool, const void *v_pool, const float *k_scales,
+                            const float *v_scales, const int32_t *table, int64_t ctx, int Hkv,
+                            int d, int bs, int quant, void *kcodes, float *ks, void *vcodes,
+                            float *vs) {
+    int64_t kv_dim = (int64_t)Hkv * d, rb = quant_row_bytes(kv_dim, quant);
+    memset(kcodes, 0, rb * ctx);
+    memset(vcodes, 0, rb * ctx);
+    for (int64_t p = 0; p < ctx; ++p) {
+        int64_t blk = table[p / bs];
+        int t = (int)(p % bs);
+        ks[p] = k_scales[blk * bs + t];
+        vs[p] = v_scales[blk * bs + t];
+        for (int h = 0; h < Hkv; ++h)
+            for (int j = 0; j < d; ++j) {
+                int64_t e = (int64_t)h * d + j;
+                int64_t ko = qk_off(blk, h, t, j, Hkv, d, quant);
+                int64_t vo = qv_off(blk, h, t, j, Hkv, d, quant);
+                if (quant == ORC_I8) {
+                    ((int8_t *)kcodes)[p * rb + e] = ((const int8_t *)k_pool)[ko];
+                    ((int8_t *)vcodes)[p * rb + e] = ((const int8_t *)v_pool)[vo];
+                } else {
+                    uint8_t *kb = (uint8_t *)kcodes + p * rb + e / 2;
+                    uint8_t *vb = (uint8_t *)vcodes + p * rb + e / 2;
+                    put_nibble(kb, (int)(e % 2), get_nibble((const uint8_t *)k_pool + ko, (j % 8) % 2));
+                    put_nibble(vb, (int)(e % 2), get_nibble((const uint8_t *)v_pool + vo, j % 2));
+                }
+            }
+    }
+}
+
+/* Paged quantized attention: gather each sequence's logical history, then
+ * orc_attention_quant per query (causal over the nq newest tokens).  q is f32
+ * [B][nq][Hq][d]; out f32 [B][nq][Hq][d]. */
+void orc_paged_attention_quant(float *out, const float *q, const void *k_pool, const void *v_pool,
+                               const float *k_scales, const float *v_scales, int quant,
+                               const int32_t *tables, const int32_t *ctx_lens, int B, int nq,
+                               int Hq, int Hkv, int d, int bs, int max_blocks, float scale) {
+    int64_t kv_dim = (int64_t)Hkv * d, rb = quant_row_bytes(kv_dim, quant);
+    for (int s = 0; s < B; ++s) {
+        int64_t ctx = ctx_lens[s] > 0 ? ctx_lens[s] : 0;
+        void *kc = malloc(rb * (ctx ? ctx : 1)), *vc = malloc(rb * (ctx ? ctx : 1));
+        float *ks = (float *)malloc(sizeof(float) * (ctx ? ctx : 1));
+        float *vs = (float *)malloc(sizeof(float) * (ctx ? ctx : 1));
+        orc_paged_gather_quant(k_pool, v_pool, k_scales, v_scales, tables + (int64_t)s * max_blocks,
+                               ctx, Hkv, d, bs, quant, kc, ks, vc, vs);
+        for (int qi = 0; qi < nq; ++qi) {
+            int64_t positions = ctx - nq + qi + 1;
+            if (positions < 0) positions = 0;
+            int64_t row = (int64_t)s * nq + qi;
+            orc_attention_quant(q + row * Hq * d, kc, ks, vc, vs, positions, Hq, Hkv, d, scale,
+                                quant, out + row * Hq * d);
+        }
+        free(kc);
+        free(vc);
+        free(ks);
+        free(vs);
+    }
+}

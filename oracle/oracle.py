@@ -18,7 +18,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB_PATH = os.path.join(_HERE, "liboracle.so")
 
-F32, F16, BF16 = 0, 1, 2
+F32, F16, BF16, I8, I4 = 0, 1, 2, 3, 4
 ERR_EXHAUSTED = -2
 ERR_UNKNOWN_SEQ = -5
 
@@ -90,6 +90,14 @@ def _declare(L):
         "orc_quantize_i8": (f32, [vp, i64, vp]),
         "orc_quantize_i4": (f32, [vp, i64, vp]),
         "orc_read_i4": (f32, [vp, i64, i64]),
+        "orc_attention_quant": (None, [vp, vp, vp, vp, vp, i64, i32, i32, i32, f32, i32, vp]),
+        "orc_quantize_tokens": (None, [vp, i64, i64, i32, vp, vp]),
+        "orc_paged_append_quant": (None, [vp, vp, vp, vp, vp, vp, vp, i64, i32, i32, i32, i32,
+                                          i64]),
+        "orc_paged_gather_quant": (None, [vp, vp, vp, vp, vp, i64, i32, i32, i32, i32, vp, vp, vp,
+                                          vp]),
+        "orc_paged_attention_quant": (None, [vp, vp, vp, vp, vp, vp, i32, vp, vp, i32, i32, i32,
+                                             i32, i32, i32, i32, f32]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
@@ -326,3 +334,74 @@ def quantize_i4(x):
 def read_i4(packed, base, i) -> float:
     packed = np.ascontiguousarray(packed, np.uint8)
     return lib().orc_read_i4(_p(packed), base, i)
+
+
+# ---------------------------------------------------------------- quantized KV (int8 / int4)
+
+def quant_row_bytes(kv_dim, quant):
+    return kv_dim if quant == I8 else (kv_dim + 1) // 2
+
+
+def quantize_tokens(src, quant):
+    """KvLayerCache::append for Int8/Int4 (cpu.rs:780-793): src [n, kv_dim] f32 ->
+    (codes [n, row_bytes] int8|uint8, scales [n] f32)."""
+    src = np.ascontiguousarray(src, np.float32)
+    n, kv_dim = src.shape
+    codes = np.zeros((n, quant_row_bytes(kv_dim, quant)), np.int8 if quant == I8 else np.uint8)
+    scales = np.zeros(n, np.float32)
+    lib().orc_quantize_tokens(_p(src), n, kv_dim, quant, _p(codes), _p(scales))
+    return codes, scales
+
+
+def attention_quant(q, kcodes, kscales, vcodes, vscales, num_heads, num_kv_heads, head_dim,
+                    quant, scale=None):
+    """attention() over an Int8/Int4 KvLayerCache (cpu.rs:1126-1151 with :798-846)."""
+    q = np.ascontiguousarray(q, np.float32)
+    if scale is None:
+        scale = np.float32(1.0) / np.sqrt(np.float32(head_dim))
+    ctx = np.zeros(num_heads * head_dim, np.float32)
+    lib().orc_attention_quant(_p(q), _p(np.ascontiguousarray(kcodes)),
+                              _p(np.ascontiguousarray(kscales, np.float32)),
+                              _p(np.ascontiguousarray(vcodes)),
+                              _p(np.ascontiguousarray(vscales, np.float32)), len(kscales),
+                              num_heads, num_kv_heads, head_dim, float(scale), quant, _p(ctx))
+    return ctx
+
+
+def quant_pool_shapes(num_blocks, Hkv, d, quant, bs=16):
+    if quant == I8:
+        return (num_blocks, Hkv, d // 8, bs, 8), (num_blocks, Hkv, d, bs)
+    return (num_blocks, Hkv, d // 8, bs, 4), (num_blocks, Hkv, d // 2, bs)
+
+
+def paged_append_quant(k_pool, v_pool, k_scales, v_scales, k_src, v_src, slots, Hkv, d, quant,
+                       bs=16):
+    slots = np.ascontiguousarray(slots, np.int64)
+    k_src = np.ascontiguousarray(k_src, np.float32)
+    v_src = np.ascontiguousarray(v_src, np.float32)
+    num_blocks = k_scales.size // bs
+    lib().orc_paged_append_quant(_p(k_pool), _p(v_pool), _p(k_scales), _p(v_scales), _p(k_src),
+                                 _p(v_src), _p(slots), len(slots), Hkv, d, bs, quant, num_blocks)
+
+
+def paged_gather_quant(k_pool, v_pool, k_scales, v_scales, table, ctx, Hkv, d, quant, bs=16):
+    rb = quant_row_bytes(Hkv * d, quant)
+    dt = np.int8 if quant == I8 else np.uint8
+    kc, vc = np.zeros((ctx, rb), dt), np.zeros((ctx, rb), dt)
+    ks, vs = np.zeros(ctx, np.float32), np.zeros(ctx, np.float32)
+    lib().orc_paged_gather_quant(_p(k_pool), _p(v_pool), _p(k_scales), _p(v_scales),
+                                 _p(np.ascontiguousarray(table, np.int32)), ctx, Hkv, d, bs, quant,
+                                 _p(kc), _p(ks), _p(vc), _p(vs))
+    return kc, ks, vc, vs
+
+
+def paged_attention_quant(q, k_pool, v_pool, k_scales, v_scales, quant, tables, ctx_lens, nq,
+                          Hq, Hkv, d, scale, bs=16):
+    q = np.ascontiguousarray(q, np.float32)
+    tables = np.ascontiguousarray(tables, np.int32)
+    ctx_lens = np.ascontiguousarray(ctx_lens, np.int32)
+    out = np.zeros((len(ctx_lens), nq, Hq, d), np.float32)
+    lib().orc_paged_attention_quant(_p(out), _p(q), _p(k_pool), _p(v_pool), _p(k_scales),
+                                    _p(v_scales), quant, _p(tables), _p(ctx_lens), len(ctx_lens),
+                                    nq, Hq, Hkv, d, bs, tables.shape[1], float(scale))
+    return out

@@ -272,3 +272,81 @@ def test_bf16_decode_matches_torch(oracle):
     assert np.array_equal(got[finite], ref[:n][finite])
     assert np.array_equal(np.isnan(got), np.isnan(ref[:n]))
     assert np.array_equal(oracle.bf16_bits(ref[:n][finite]), bits[:n][finite])
+
+
+# ---------------------------------------------------------------- quantized KV attention
+
+def _ref_quant_case():
+    """The inputs of cpu.rs:1480-1544 (int8_/int4_kv_attention_close_to_full)."""
+    g = GOLD["kv_quant_attention_close_to_full"]
+    Hq, Hkv, d, P = g["num_heads"], g["num_kv_heads"], g["head_dim"], g["positions"]
+    kv = Hkv * d
+    k = np.array([[((p + i) % 7) * 0.3 - 1.0 for i in range(kv)] for p in range(P)], np.float32)
+    v = np.array([[((p * 2 + i) % 5) * 0.5 for i in range(kv)] for p in range(P)], np.float32)
+    q = np.array([(i % 3) * 0.2 for i in range(Hq * d)], np.float32)
+    return g, Hq, Hkv, d, k, v, q
+
+
+@pytest.mark.parametrize("quant,tol_key", [(3, "tol_int8"), (4, "tol_int4")])
+def test_quant_attention_close_to_full_reference_case(oracle, quant, tol_key):
+    g, Hq, Hkv, d, k, v, q = _ref_quant_case()
+    full = oracle.attention(q, k, v, Hq, Hkv, d)
+    kc, ks = oracle.quantize_tokens(k, quant)
+    vc, vs = oracle.quantize_tokens(v, quant)
+    qa = oracle.attention_quant(q, kc, ks, vc, vs, Hq, Hkv, d, quant)
+    assert np.abs(full - qa).max() <= g[tol_key]
+
+
+@pytest.mark.parametrize("quant", [3, 4])
+def test_quant_attention_matches_dequantized_f64(oracle, quant):
+    """Quantized attention == textbook attention over the dequantized codes."""
+    rng = np.random.default_rng(50 + quant)
+    Hq, Hkv, d, P = 8, 2, 16, 40
+    k = rng.standard_normal((P, Hkv * d)).astype(np.float32)
+    v = rng.standard_normal((P, Hkv * d)).astype(np.float32)
+    q = rng.standard_normal(Hq * d).astype(np.float32)
+    kc, ks = oracle.quantize_tokens(k, quant)
+    vc, vs = oracle.quantize_tokens(v, quant)
+    if quant == 3:
+        kd, vd = kc.astype(np.float32) * ks[:, None], vc.astype(np.float32) * vs[:, None]
+    else:
+        dq = lambda c, s: np.array([[oracle.read_i4(c[p], 0, i) for i in range(Hkv * d)]
+                                    for p in range(P)], np.float32) * s[:, None]
+        kd, vd = dq(kc, ks), dq(vc, vs)
+    got = oracle.attention_quant(q, kc, ks, vc, vs, Hq, Hkv, d, quant)
+    ref = brute_attention_f64(q, kd, vd, Hq, Hkv, d, 1 / np.sqrt(d))
+    assert np.abs(got - ref).max() < 1e-5
+
+
+@pytest.mark.parametrize("quant", [3, 4])
+def test_paged_quant_round_trip_and_attention(oracle, quant):
+    """Paged quantized append -> gather reproduces the contiguous codes and scales
+    byte for byte; paged attention equals contiguous quantized attention bitwise."""
+    rng = np.random.default_rng(60 + quant)
+    Hq, Hkv, d, nb, ntok = 8, 2, 32, 12, 70
+    ks_shape, vs_shape = oracle.quant_pool_shapes(nb, Hkv, d, quant)
+    dt = np.int8 if quant == 3 else np.uint8
+    kp = rng.integers(-100, 100, ks_shape).astype(dt)
+    vp = rng.integers(-100, 100, vs_shape).astype(dt)
+    ksc = rng.standard_normal(nb * 16).astype(np.float32)
+    vsc = rng.standard_normal(nb * 16).astype(np.float32)
+    table = rng.permutation(nb)[: -(-ntok // 16)].astype(np.int32)
+    k = rng.standard_normal((ntok, Hkv * d)).astype(np.float32)
+    v = rng.standard_normal((ntok, Hkv * d)).astype(np.float32)
+    slots = np.array([table[p // 16] * 16 + p % 16 for p in range(ntok)], np.int64)
+    oracle.paged_append_quant(kp, vp, ksc, vsc, k[:33], v[:33], slots[:33], Hkv, d, quant)
+    oracle.paged_append_quant(kp, vp, ksc, vsc, k[33:], v[33:], slots[33:], Hkv, d, quant)
+    kc, ks = oracle.quantize_tokens(k, quant)
+    vc, vs = oracle.quantize_tokens(v, quant)
+    gkc, gks, gvc, gvs = oracle.paged_gather_quant(kp, vp, ksc, vsc, table, ntok, Hkv, d, quant)
+    assert np.array_equal(gkc, kc) and np.array_equal(gvc, vc)
+    assert np.array_equal(gks, ks) and np.array_equal(gvs, vs)
+    q = rng.standard_normal((1, 2, Hq, d)).astype(np.float32)
+    tables = np.zeros((1, 8), np.int32)
+    tables[0, :len(table)] = table
+    out = oracle.paged_attention_quant(q, kp, vp, ksc, vsc, quant, tables, np.array([ntok], np.int32),
+                                       2, Hq, Hkv, d, 0.25)
+    for j in range(2):
+        n = ntok - 2 + j + 1
+        ref = oracle.attention_quant(q[0, j], kc[:n], ks[:n], vc[:n], vs[:n], Hq, Hkv, d, quant, 0.25)
+        assert np.array_equal(out[0, j].reshape(-1), ref)
