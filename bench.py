@@ -26,7 +26,7 @@ import json
 import os
 import sys
 import time
-from dataclasses import dataclass, field
+from dataclasses import dataclass, field, replace
 
 import numpy as np
 
@@ -51,6 +51,7 @@ class Workload:
     prefill_seqs: int = 0  # chunked-prefill sequences appending alongside
     prefill_chunk: int = 0
     extras: list = field(default_factory=list)  # "fork", "swap"
+    quant: str = "none"  # KV storage: "none" (dtype above), "int8", "int4" (dlm's --kv-quant)
 
 
 WORKLOADS = {
@@ -78,6 +79,9 @@ def parse():
     p.add_argument("--warmup", type=int, default=500,
                    help="untimed steps run before each timed region (lets clocks settle)")
     p.add_argument("--workload", default="config2", choices=sorted(WORKLOADS))
+    p.add_argument("--kv-quant", default="none", choices=["none", "int8", "int4"],
+                   help="store K/V as per-token-scaled int8/int4 codes (dlm's --kv-quant); "
+                        "queries and new tokens stay f16")
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--only", choices=["step", "unfused", "attention", "append"],
                    help="time one phase only (for profiling runs)")
@@ -91,23 +95,33 @@ def parse():
 
 
 def elem_bytes(w):
+    """Bytes of one query / new-token / output element."""
     return 4 if w.dtype == "f32" else 2
 
 
+def kv_token_bytes(w):
+    """Stored bytes of one token of one pool (all kv heads): elements, or codes
+    plus the token's f32 scale."""
+    if w.quant == "none":
+        return w.hkv * w.d * elem_bytes(w)
+    return w.hkv * w.d * (1 if w.quant == "int8" else 0.5) + 4
+
+
 def attn_bytes(w, ctx, out_bytes):
-    """Algorithmic bytes of one attention launch: K+V read, Q read, out write,
-    block table and context lengths."""
+    """Algorithmic bytes of one attention launch: K+V read (with scales when
+    quantized), Q read, out write, block table and context lengths."""
     ctx = np.asarray(ctx, np.int64)
     eb = elem_bytes(w)
-    kv = int(ctx.sum()) * 2 * w.hkv * w.d * eb
+    kv = int(int(ctx.sum()) * 2 * kv_token_bytes(w))
     qo = len(ctx) * w.nq * w.hq * w.d * (eb + out_bytes)
     meta = int(((ctx + BS - 1) // BS).sum()) * 4 + len(ctx) * 4
     return kv + qo + meta
 
 
 def append_bytes(w, n_tok):
-    """Per appended token: K+V read, the same written, and an 8-byte slot."""
-    return n_tok * (2 * (2 * w.hkv * w.d * elem_bytes(w)) + 8)
+    """Per appended token: K+V read, K+V stored (codes and scale when
+    quantized), and an 8-byte slot."""
+    return n_tok * (2 * (w.hkv * w.d * elem_bytes(w) + kv_token_bytes(w)) + 8)
 
 
 def copy_calibration(torch, ops, steps):
@@ -134,23 +148,36 @@ def cpu_baseline(w, budget_s):
     npdt = np.float32 if w.dtype == "f32" else np.float16
     X = 16 // np.dtype(npdt).itemsize
     done_tok, done_seq, elapsed, nbytes = 0, 0, 0.0, 0
+    qcode = {"int8": orc.I8, "int4": orc.I4}.get(w.quant)
     while elapsed < budget_s and done_seq < 4096:
         c = int(rng.integers(w.ctx[0], w.ctx[1] + 1))
         nb = -(-c // BS)
-        kp = (rng.standard_normal((nb, w.hkv, w.d // X, BS, X)) * 0.5).astype(npdt)
-        vp = (rng.standard_normal((nb, w.hkv, w.d, BS)) * 0.5).astype(npdt)
         table = rng.permutation(nb).astype(np.int32)[None]
         q = (rng.standard_normal((1, w.nq, w.hq, w.d)) * 0.5).astype(npdt)
-        t0 = time.perf_counter()
-        orc.paged_attention(q, kp, vp, table, np.array([c], np.int32), w.nq, w.hq, w.hkv, w.d, BS,
-                            1.0 / np.sqrt(w.d))
+        if qcode is None:
+            kp = (rng.standard_normal((nb, w.hkv, w.d // X, BS, X)) * 0.5).astype(npdt)
+            vp = (rng.standard_normal((nb, w.hkv, w.d, BS)) * 0.5).astype(npdt)
+            t0 = time.perf_counter()
+            orc.paged_attention(q, kp, vp, table, np.array([c], np.int32), w.nq, w.hq, w.hkv, w.d,
+                                BS, 1.0 / np.sqrt(w.d))
+        else:
+            ks, vs = orc.quant_pool_shapes(nb, w.hkv, w.d, qcode)
+            kp = rng.integers(0, 256, ks, dtype=np.uint8)
+            vp = rng.integers(0, 256, vs, dtype=np.uint8)
+            ksc = rng.random((nb, BS), dtype=np.float32) * 0.02
+            vsc = rng.random((nb, BS), dtype=np.float32) * 0.02
+            t0 = time.perf_counter()
+            orc.paged_attention_quant(q.astype(np.float32), kp, vp, ksc, vsc, qcode, table,
+                                      np.array([c], np.int32), w.nq, w.hq, w.hkv, w.d,
+                                      1.0 / np.sqrt(w.d))
         elapsed += time.perf_counter() - t0
         done_tok += c
         done_seq += 1
         nbytes += attn_bytes(w, [c], elem_bytes(w))
     return {
         "value": round(nbytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-        "sample": (f"oracle/oracle.c paged attention (f32 restatement of dlm attention(), "
+        "sample": (f"oracle/oracle.c paged attention{'' if qcode is None else ' over ' + w.quant + ' pools'} "
+                   f"(f32 restatement of dlm attention(), "
                    f"1 thread) over {done_seq} {w.name} sequences, {done_tok} context tokens, "
                    f"{elapsed:.1f} s; same algorithmic-bytes formula"),
         "context_tokens_per_s": round(done_tok / elapsed, 1),
@@ -218,6 +245,10 @@ def main():
         copy_calibration(torch, ops, args.steps)
         return
     w = WORKLOADS[args.workload]
+    if args.kv_quant != "none":
+        if w.dtype != "f16":
+            sys.exit(f"--kv-quant needs an f16 workload ({w.name} is {w.dtype})")
+        w = replace(w, quant=args.kv_quant, extras=[])
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     gen = torch.Generator(device=dev)
@@ -233,17 +264,47 @@ def main():
     pool_blocks = max(floor, int(need * (1.6 if "fork" in w.extras else 1.2)) + 64)
     cfg = KvCacheConfig(num_layers=w.layers, num_kv_heads=w.hkv, head_dim=w.d, block_size=BS)
     cache = PagedKvCache.with_seeded_shuffle(cfg, pool_blocks, seed=SEED)
-    geom = ops.PoolGeometry(pool_blocks, w.hkv, w.d, BS, tdt)
-    layers = ops.alloc_pools(geom, dev, num_layers=w.layers)
-    for kp, vp in layers:
-        kp.normal_(0.0, 0.5, generator=gen)
-        vp.normal_(0.0, 0.5, generator=gen)
+    quant = w.quant != "none"
+    if quant:
+        # Quantized pools: every slot filled by the quantizing append itself.
+        layers = [ops.alloc_quant_pools(pool_blocks, w.hkv, w.d, w.quant, dev)
+                  for _ in range(w.layers)]
+        fill = torch.arange(pool_blocks * BS, dtype=torch.int64, device=dev)
+        for kv in layers:
+            for lo in range(0, fill.numel(), 65536):
+                sl = fill[lo:lo + 65536]
+                src = torch.randn((sl.numel(), w.hkv, w.d), generator=gen, device=dev,
+                                  dtype=tdt) * 0.5
+                ops.kv_append_quant(kv, src, src.flip(0), sl, num_kv_heads=w.hkv, head_dim=w.d)
+        del fill
+    else:
+        geom = ops.PoolGeometry(pool_blocks, w.hkv, w.d, BS, tdt)
+        layers = ops.alloc_pools(geom, dev, num_layers=w.layers)
+        for kp, vp in layers:
+            kp.normal_(0.0, 0.5, generator=gen)
+            vp.normal_(0.0, 0.5, generator=gen)
 
     t_books = time.perf_counter()
     batches = [Batch(torch, w, cache, b * 1000, ctxs[b], dev, gen, tdt) for b in range(2)]
     books_s = time.perf_counter() - t_books
     max_blocks = -(-w.ctx[1] // BS)
     ws = ops.alloc_workspace(ops.attention_workspace_bytes(w.batch, w.nq, w.hq, w.d, max_blocks), dev)
+
+    def append_quant(bt):
+        for kv in layers:
+            ops.kv_append_quant(kv, bt.k_new, bt.v_new, bt.slots, num_kv_heads=w.hkv, head_dim=w.d)
+
+    def attend_quant(bt):
+        for kv in layers:
+            ops.paged_decode_attention_quant(bt.q, kv, bt.tables, bt.lens, num_kv_heads=w.hkv,
+                                             out=bt.out, workspace=ws)
+
+    def step_quant(bt):
+        # No fused append into quantized pools: quantizing append, then attention.
+        for kv in layers:
+            ops.kv_append_quant(kv, bt.k_new, bt.v_new, bt.slots, num_kv_heads=w.hkv, head_dim=w.d)
+            ops.paged_decode_attention_quant(bt.q, kv, bt.tables, bt.lens, num_kv_heads=w.hkv,
+                                             out=bt.out, workspace=ws)
 
     def append(bt):
         for kp, vp in layers:
@@ -271,6 +332,8 @@ def main():
             ops.paged_decode_step(bt.q, bt.k_dec, bt.v_dec, kp, vp, bt.tables, bt.lens,
                                   num_kv_heads=w.hkv, out=bt.out, workspace=ws)
 
+    if quant:
+        step, step_unfused, attend, append = step_quant, None, attend_quant, append_quant
     for i in range(args.warmup):
         step(batches[i & 1])
     torch.cuda.synchronize()
@@ -304,7 +367,7 @@ def main():
         return a.elapsed_time(b) / (reps * (n // reps))
 
     def phase(name, fn, reps, n):
-        if args.only not in (None, name):
+        if args.only not in (None, name) or fn is None:
             return float("nan")
         return timed(capture(fn, reps), reps, n)
 
@@ -332,18 +395,18 @@ def main():
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(step_ms, 5),
-        "ms_per_step_unfused": round(unfused_ms, 5),
+        "ms_per_step_unfused": None if quant else round(unfused_ms, 5),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": w.dtype,
+        "dtype": w.dtype if not quant else f"{w.quant} KV codes (f16 q, f16 MFMA operands)",
         "data": "synthetic (seeded N(0,1)*0.5 K/V/Q, seeded contexts and shuffled pool)",
         "config": {
             "workload": w.about,
             "num_q_heads": w.hq, "num_kv_heads": w.hkv, "head_dim": w.d, "block_size": BS,
             "layers": w.layers, "batch": w.batch, "queries_per_seq": w.nq,
             "ctx": f"U[{w.ctx[0]},{w.ctx[1]}] seed {SEED}", "pool_blocks": pool_blocks,
-            "rotating_batches": 2, "mean_context_tokens": float(ctx_tok),
+            "kv_quant": w.quant, "rotating_batches": 2, "mean_context_tokens": float(ctx_tok),
             "appended_tokens_per_step": n_app, "parallelism": "single GPU",
         },
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),
@@ -363,9 +426,11 @@ def main():
         "wall_s_timed_region": round(wall_s, 4),
         "timing": f"HIP events around replays of HIP graphs of {REPS} steps each ({5 * REPS} "
                   "appends for the append-only line), alternating the two batches; a step is "
-                  "dlmk_paged_decode_step (append + attention in one launch), "
-                  "ms_per_step_unfused the same step as dlmk_kv_append + "
-                  "dlmk_paged_decode_attention",
+                  + ("dlmk_kv_append_quant + dlmk_paged_decode_attention_quant (no fused "
+                     "step for quantized pools)" if quant else
+                     "dlmk_paged_decode_step (append + attention in one launch), "
+                     "ms_per_step_unfused the same step as dlmk_kv_append + "
+                     "dlmk_paged_decode_attention"),
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
@@ -378,7 +443,16 @@ def main():
         result["swap"] = bench_swap(torch, ops, cache, layers[0], batches[0], w, dev)
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(w, args.cpu_seconds)
-    print(json.dumps(result), flush=True)
+    print(json.dumps(_finite(result)), flush=True)
+
+
+def _finite(x):
+    """NaN (a phase skipped by --only) becomes null: the line stays valid JSON."""
+    if isinstance(x, dict):
+        return {k: _finite(v) for k, v in x.items()}
+    if isinstance(x, float) and x != x:
+        return None
+    return x
 
 
 def _events(torch, fn, n):

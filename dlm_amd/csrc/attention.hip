@@ -54,6 +54,10 @@ constexpr float kLog2e = 1.4426950408889634f;
 #ifndef DLMK_MFMA_PD
 #define DLMK_MFMA_PD 2
 #endif
+// Prefetch depth for int8 / int4 pools, whose tiles are 2x / 4x smaller.
+#ifndef DLMK_MFMA_PDQ
+#define DLMK_MFMA_PDQ 2
+#endif
 // Minimum waves per SIMD the register allocation must allow (0: compiler's choice).
 #ifndef DLMK_MFMA_WPE
 #define DLMK_MFMA_WPE 0
@@ -220,12 +224,34 @@ struct Mfma<__bf16> {
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
+// Exact widening of small integer codes to f16 without conversions: the f16
+// with bit pattern 0x64uu is 1024 + uu for any byte uu, so biasing a code c
+// to the unsigned byte c + B and placing it under a 0x64 high byte yields
+// 1024 + B + c, and one packed f16 subtraction of 1024 + B leaves c.
+// v_perm_b32 builds two such halves from bytes lo, lo+1 of w in one op.
+template <int BIAS, int LO>
+__device__ __forceinline__ f16x2 widen_pair(uint32_t w) {
+    constexpr uint32_t sel = 0x04000400u | (uint32_t)LO | (uint32_t)(LO + 1) << 16;
+    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, w, sel);
+    return __builtin_bit_cast(f16x2, h) - f16x2{(_Float16)(1024 + BIAS), (_Float16)(1024 + BIAS)};
+}
+
+// Four biased byte codes (bytes 0..3 of w) -> f16x4.
+template <int BIAS>
+__device__ __forceinline__ f16x4 widen4(uint32_t w) {
+    const f16x2 a = widen_pair<BIAS, 0>(w), b = widen_pair<BIAS, 2>(w);
+    return f16x4{a[0], a[1], b[0], b[1]};
+}
+
 // Storage codecs of the matrix-core kernel: where a lane's K chunk (8
 // consecutive dims of one token: the A operand of S^T = K.Q^T) and V piece (4
 // consecutive tokens of one dim: the B operand of O = P.V) sit in a (block,
-// kv head) tile, and how they widen to MFMA operands.  Quantized codecs keep
-// one f32 scale per token (K scales fold into the score, V scales multiply
-// the widened values); codes widen to f16 exactly (|code| <= 127).
+// kv head) tile, and how they widen to MFMA operands.
+//   q_op: a fixed permutation of the 8 dims of a Q operand chunk, matching
+//     the order k_op emits a K chunk in (the dot product does not care).
+//   Quantized codecs keep one f32 scale per token: K scales multiply the
+//     score, V scales multiply the probabilities (p * v_scale, 4 values per
+//     lane, instead of 32 widened values).  Codes widen to f16 exactly.
 template <typename E>
 struct CodecFloat {  // f16 / bf16 pools: [d/8][16][8] and [d][16] elements
     using QT = E;
@@ -240,12 +266,9 @@ struct CodecFloat {  // f16 / bf16 pools: [d/8][16][8] and [d][16] elements
     static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int g, int n) {
         return stream_load(reinterpret_cast<const VRaw *>(tile) + ((16 * k + n) * kBlock + 4 * g) / 4);
     }
+    static __device__ __forceinline__ KRaw q_op(KRaw q) { return q; }
     static __device__ __forceinline__ typename Op::x8 k_op(KRaw r) { return r; }
-    static __device__ __forceinline__ typename Op::x4 v_op(VRaw r, f32x4, int, int g, int valid) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) r[e] = (4 * g + e < valid) ? r[e] : E(0.f);
-        return r;
-    }
+    static __device__ __forceinline__ typename Op::x4 v_op(VRaw r, int) { return r; }
 };
 
 struct CodecI8 {  // int8 pools: K [d/8][16][8] bytes, V [d][16] bytes
@@ -261,52 +284,40 @@ struct CodecI8 {  // int8 pools: K [d/8][16][8] bytes, V [d][16] bytes
     static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int g, int n) {
         return stream_load(reinterpret_cast<const VRaw *>(tile + (16 * k + n) * kBlock + 4 * g));
     }
+    static __device__ __forceinline__ f16x8 q_op(f16x8 q) { return q; }
     static __device__ __forceinline__ f16x8 k_op(KRaw r) {
-        f16x8 o;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = (_Float16)(int8_t)(r[e / 4] >> (8 * (e % 4)));
-        return o;
+        const f16x4 a = widen4<128>(r[0] ^ 0x80808080u), b = widen4<128>(r[1] ^ 0x80808080u);
+        return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     }
-    static __device__ __forceinline__ f16x4 v_op(VRaw r, f32x4 vs, int, int g, int valid) {
-        f16x4 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float v = (float)(int8_t)(r >> (8 * e)) * vs[e];
-            o[e] = (_Float16)(4 * g + e < valid ? v : 0.f);
-        }
-        return o;
-    }
+    static __device__ __forceinline__ f16x4 v_op(VRaw r, int) { return widen4<128>(r ^ 0x80808080u); }
 };
 
-struct CodecI4 {  // int4 pools: K [d/8][16][4] bytes, V [d/2][16] bytes (two dims per byte)
+struct CodecI4 {  // int4 pools: K [d/8][16][4] bytes (two elements a byte, low nibble even), V [d/2][16] bytes
     using QT = _Float16;
     using Op = Mfma<_Float16>;
     using KRaw = uint32_t;
     using VRaw = uint32_t;
     static constexpr bool kScaled = true;
     static constexpr int kTileBytesPerDim = kBlock / 2;
-    static __device__ __forceinline__ int sext4(uint32_t nib) { return (int)(nib ^ 8u) - 8; }
     static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int i, int lane) {
         return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * i + lane);
     }
     static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int g, int n) {
         return stream_load(reinterpret_cast<const VRaw *>(tile + ((16 * k + n) >> 1) * kBlock + 4 * g));
     }
-    static __device__ __forceinline__ f16x8 k_op(KRaw r) {
-        f16x8 o;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) o[e] = (_Float16)sext4((r >> (4 * e)) & 0xfu);
-        return o;
+    // k_op emits elements in the order 0 2 4 6 1 3 5 7 (even nibbles, then odd).
+    static __device__ __forceinline__ f16x8 q_op(f16x8 q) {
+        return f16x8{q[0], q[2], q[4], q[6], q[1], q[3], q[5], q[7]};
     }
-    static __device__ __forceinline__ f16x4 v_op(VRaw r, f32x4 vs, int n, int g, int valid) {
-        f16x4 o;
-        const int sh = 4 * (n & 1);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const float v = (float)sext4((r >> (8 * e + sh)) & 0xfu) * vs[e];
-            o[e] = (_Float16)(4 * g + e < valid ? v : 0.f);
-        }
-        return o;
+    static __device__ __forceinline__ f16x8 k_op(KRaw r) {
+        const uint32_t x = r ^ 0x88888888u;  // signed nibble c -> c + 8
+        const f16x4 a = widen4<8>(x & 0x0f0f0f0fu), b = widen4<8>((x >> 4) & 0x0f0f0f0fu);
+        return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    }
+    // Byte t of a V row holds dims 2p (low nibble) and 2p + 1 of token t; lane
+    // dim n takes nibble n & 1 of each of its 4 tokens.
+    static __device__ __forceinline__ f16x4 v_op(VRaw r, int n) {
+        return widen4<8>(((r >> (4 * (n & 1))) & 0x0f0f0f0fu) ^ 0x08080808u);
     }
 };
 
@@ -358,13 +369,16 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     const int nblk_seq = (ctx + kBlock - 1) / kBlock;
     const int32_t *table = block_tables + (int64_t)seq * max_blocks;
 
-    // Q^T operand: row n of the group, dims 32i + 8g .. +7 (zero beyond ROWS).
+    // Q^T operand: row n of the group, dims 32i + 8g .. +7 (zeroed beyond
+    // ROWS below).  Lanes past ROWS load row n % ROWS, so the loads carry no
+    // branches (a masked load would make its first use wait for it).
     x8 qb[KI];
     {
-        const int j = n / GQA, h = kvh * GQA + n % GQA;
+        const int r = n % ROWS;
+        const int j = r / GQA, h = kvh * GQA + r % GQA;
         const x8 *qp = reinterpret_cast<const x8 *>(q + ((int64_t)(seq * NQ + j) * num_q_heads + h) * D);
 #pragma unroll
-        for (int i = 0; i < KI; ++i) qb[i] = n < ROWS ? qp[g + 4 * i] : x8{};
+        for (int i = 0; i < KI; ++i) qb[i] = qp[g + 4 * i];
     }
     // Causal limit of this lane's row (verify query n / GQA).
     const int limit = n < ROWS ? ctx - NQ + n / GQA + 1 : ctx;
@@ -378,10 +392,19 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     int64_t blk[NB];
     bool ok[NB];
     int nvalid = 0;
+    // The table reads are unconditional (index clamped into the row), so the
+    // NB scalar loads go out back to back and share one wait; a guarded read
+    // per block would serialise NB memory round trips before the first tile.
+    int32_t raw[NB];
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
         const int lb = part * (NW * NB) + b * NW + wave;
-        const int64_t id = lb < nblk_seq ? (int64_t)table[lb] : -1;
+        raw[b] = table[max(min(lb, nblk_seq - 1), 0)];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int lb = part * (NW * NB) + b * NW + wave;
+        const int64_t id = lb < nblk_seq ? (int64_t)raw[b] : -1;
         lbs[b] = lb;
         ok[b] = id >= 0 && id < num_blocks;
         blk[b] = id;
@@ -423,23 +446,35 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         typename C::KRaw kb[NB][KI];
         typename C::VRaw vb[NB][VN];
         f32x4 ksc[NB], vsc[NB];
+        // A stage's scale load goes out before its code loads, fenced by a
+        // scheduling barrier: loads complete in issue order, so waiting for
+        // a scale never waits for a later stage's codes.
         auto issue = [&](int t) {
             if (t < NB) {
+                if constexpr (C::kScaled) {
+                    ksc[t] = *reinterpret_cast<const f32x4 *>(k_scales + blk[t] * kBlock + 4 * g);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 const uint8_t *kt = k_pool + (blk[t] * num_kv_heads + kvh) * TILE;
 #pragma unroll
                 for (int i = 0; i < KI; ++i) kb[t][i] = C::load_k(kt, i, lane);
-                if constexpr (C::kScaled)
-                    ksc[t] = *reinterpret_cast<const f32x4 *>(k_scales + blk[t] * kBlock + 4 * g);
             } else if (t < 2 * NB) {
+                if constexpr (C::kScaled) {
+                    vsc[t - NB] = *reinterpret_cast<const f32x4 *>(v_scales + blk[t - NB] * kBlock + 4 * g);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
                 const uint8_t *vt = v_pool + (blk[t - NB] * num_kv_heads + kvh) * TILE;
 #pragma unroll
                 for (int k = 0; k < VN; ++k) vb[t - NB][k] = C::load_v(vt, k, g, n);
-                if constexpr (C::kScaled)
-                    vsc[t - NB] = *reinterpret_cast<const f32x4 *>(v_scales + blk[t - NB] * kBlock + 4 * g);
             }
         };
 #pragma unroll
         for (int t = 0; t < PD; ++t) issue(t);
+        __builtin_amdgcn_sched_barrier(0);
+        // Q operand in the order k_op emits K (zero rows past ROWS), after the
+        // first tile loads are out.
+#pragma unroll
+        for (int i = 0; i < KI; ++i) qb[i] = n < ROWS ? C::q_op(qb[i]) : x8{};
 
         // Scores S^T: s[b][j] = row n, token 4g + j of block b.
         float s[NB][4];
@@ -467,25 +502,46 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         m = fmaxf(m, __shfl_xor(m, 16));
         m = fmaxf(m, __shfl_xor(m, 32));
 
-        // O += P . V; P rounded to the operand type, and l sums the rounded P.
+        // O += P . V.  Float pools: P rounded to the operand type, and l sums
+        // the rounded P.  Quantized pools: the operand is p * v_scale (l sums
+        // p), so the widened codes need no per-element scaling.
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
             issue(NB + b + PD);
             __builtin_amdgcn_sched_barrier(0);
+            // Tokens at or past `valid` are outside the context (stale bytes,
+            // maybe NaN) or belong to a masked block (another block's bytes).
+            const int valid = __builtin_amdgcn_readfirstlane(ok[b] ? ctx - lbs[b] * kBlock : 0);
             x4 pa;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const PT ph = (PT)(m == -INFINITY ? 0.f : exp2f(s[b][j] - m));
-                pa[j] = ph;
-                lsum += (float)ph;
+                const float p = m == -INFINITY ? 0.f : exp2f(s[b][j] - m);
+                if constexpr (C::kScaled) {
+                    // p is 0 there already; the select keeps a NaN scale out.
+                    pa[j] = (PT)(4 * g + j < valid ? p * vsc[b][j] : 0.f);
+                    lsum += p;
+                } else {
+                    const PT ph = (PT)p;
+                    pa[j] = ph;
+                    lsum += (float)ph;
+                }
             }
-            // Tokens past the context hold stale bytes (maybe NaN), and masked
-            // blocks hold another block's bytes: v_op zeroes them so p = 0
-            // contributes exactly nothing.
-            const int valid = ok[b] ? ctx - lbs[b] * kBlock : 0;
+            typename M::x4 vo[VN];
 #pragma unroll
-            for (int k = 0; k < VN; ++k)
-                acc[k] = M::pv(pa, C::v_op(vb[b][k], vsc[b], n, g, valid), acc[k]);
+            for (int k = 0; k < VN; ++k) vo[k] = C::v_op(vb[b][k], n);
+            if constexpr (!C::kScaled) {
+                // Float V can hold NaN past the context, and 0 * NaN is NaN:
+                // zero it.  A wave-uniform branch, taken only by partial blocks.
+                if (valid < kBlock) {
+#pragma unroll
+                    for (int k = 0; k < VN; ++k)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            vo[k][e] = 4 * g + e < valid ? vo[k][e] : (PT)0.f;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < VN; ++k) acc[k] = M::pv(pa, vo[k], acc[k]);
             __builtin_amdgcn_sched_barrier(0);
         }
     }
@@ -554,10 +610,13 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
     const int32_t *table = block_tables + (int64_t)seq * max_blocks;
 
     int64_t blk[BPW];
+    int32_t raw[BPW];
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) raw[b] = table[max(min(first_lb + b, nblk_seq - 1), 0)];
 #pragma unroll
     for (int b = 0; b < BPW; ++b) {
         const int lb = first_lb + b;
-        int64_t id = lb < nblk_seq ? (int64_t)table[lb] : -1;
+        int64_t id = lb < nblk_seq ? (int64_t)raw[b] : -1;
         blk[b] = (id >= 0 && id < num_blocks) ? id : -1;
     }
     if (k_new != nullptr) {
@@ -814,7 +873,8 @@ int launch_pair(const Args &a, int partition, Launch launch) {
 // Matrix-core path: NW waves x NB blocks per partition, pool format C.
 template <typename C, int D, int GQA, int NQ>
 int launch_mfma(const Args &a) {
-    constexpr int NW = DLMK_MFMA_NW, NB = DLMK_MFMA_NB, PD = DLMK_MFMA_PD;
+    constexpr int NW = DLMK_MFMA_NW, NB = DLMK_MFMA_NB;
+    constexpr int PD = C::kScaled ? DLMK_MFMA_PDQ : DLMK_MFMA_PD;
     static_assert(NW * NB * kBlock >= kMinPartition, "partition below the workspace bound");
     using QT = typename C::QT;
     return launch_pair<D>(a, NW * NB * kBlock, [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {

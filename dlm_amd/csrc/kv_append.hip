@@ -66,70 +66,121 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(
 
 }  // namespace
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
 // ---------------------------------------------------------------------------
 // Quantizing append for int8 / int4 pools (dlmk_kv_append_quant).
 //
 // KvLayerCache::append for the Int8 / Int4 stores (src/forward/cpu.rs:780-793,
-// quantize_i8 / quantize_i4 at :667-700): each token's K (and V) vector over
+// quantize_i8 / quantize_i4 at :672-701): each token's K (and V) vector over
 // the whole kv_dim gets one scale max|x| / 127 (or / 7) and codes
-// round(x / scale) clamped to +-127 (+-7), an all-zero vector scale 0.  One
-// wavefront per token: a wave max-reduction, then the codes go to the paged
-// layout -- int8 K [d/8][16][8], V [d][16]; int4 K [d/8][16][4] and
-// V [d/2][16] bytes holding two consecutive dims of one token (low nibble for
-// the even dim), so a byte never mixes tokens and appends never share one.
+// round(x / scale) clamped to +-127 (+-7) -- NaN quotients give code 0, as
+// Rust's saturating `as i8` does -- and an all-zero vector scale 0.
+//
+// One wavefront per token.  Lane l owns the 8-dim chunks l, l + 64, ... of
+// the token (NC of them, kept in registers): one 16-byte source load per chunk
+// (two for f32), a wave max-reduction, then one store per chunk for K
+// (int8 K [d/8][16][8]: 8 bytes; int4 K [d/8][16][4]: 4 bytes) and 8 / 4 byte
+// stores for V (int8 V [d][16]; int4 V [d/2][16], a byte holding dims 2p and
+// 2p + 1 of one token, low nibble 2p, so a byte never mixes tokens and
+// appends never share one).
 // ---------------------------------------------------------------------------
 template <typename S>
-__device__ __forceinline__ float to_f32(S x) {
-    return (float)x;
+__device__ __forceinline__ void load8(const S *p, float (&x)[8]) {
+    if constexpr (sizeof(S) == 4) {
+        const u32x4 a = reinterpret_cast<const u32x4 *>(p)[0];
+        const u32x4 b = reinterpret_cast<const u32x4 *>(p)[1];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            x[k] = __uint_as_float(a[k]);
+            x[4 + k] = __uint_as_float(b[k]);
+        }
+    } else {
+        const u32x4 raw = *reinterpret_cast<const u32x4 *>(p);
+        S e[8];
+        __builtin_memcpy(e, &raw, 16);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) x[k] = (float)e[k];
+    }
 }
 
-template <int QBITS, typename S>
+__device__ __forceinline__ int quant_code(float x, float inv_ok, float scale, float qmax) {
+    const float r = roundf(x / scale);
+    return (inv_ok == 0.f || r != r) ? 0 : (int)fminf(fmaxf(r, -qmax), qmax);
+}
+
+template <int QBITS, typename S, int NC>
 __global__ __launch_bounds__(256) void kv_append_quant_kernel(
     uint8_t *__restrict__ k_pool, uint8_t *__restrict__ v_pool, float *__restrict__ k_scales,
     float *__restrict__ v_scales, const S *__restrict__ k_src, const S *__restrict__ v_src,
     const int64_t *__restrict__ slots, int64_t n_tok, int num_kv_heads, int head_dim,
-    int block_size, int64_t num_slots) {
+    int64_t num_slots) {
+    constexpr int BS = 16;
     const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     if (tok >= n_tok) return;
     const int64_t slot = slots[tok];
     if (slot < 0 || slot >= num_slots) return;
-    const int64_t blk = slot / block_size;
-    const int t = (int)(slot - blk * block_size);
-    const int d = head_dim, kv_dim = num_kv_heads * head_dim;
+    const int64_t blk = slot / BS;
+    const int t = (int)(slot - blk * BS);
+    const int d = head_dim, kv_dim = num_kv_heads * head_dim, nchunks = kv_dim / 8;
     const float qmax = QBITS == 8 ? 127.f : 7.f;
-    const int64_t tile_bytes = (int64_t)d * block_size * QBITS / 8;
+    const int64_t tile_bytes = (int64_t)d * BS * QBITS / 8;
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
         const S *src = (which ? v_src : k_src) + tok * kv_dim;
         uint8_t *pool = which ? v_pool : k_pool;
+        float x[NC][8];
         float mx = 0.f;
-        for (int e = lane; e < kv_dim; e += 64) mx = fmaxf(mx, fabsf(to_f32(src[e])));
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c = lane + 64 * i;
+            if (c < nchunks) {
+                load8(src + 8 * c, x[i]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) x[i][k] = 0.f;
+            }
+#pragma unroll
+            for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(x[i][k]));
+        }
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
         const float scale = mx / qmax;
-        const bool zero = !(scale > 0.f);
-        if (lane == 0) (which ? v_scales : k_scales)[slot] = zero ? 0.f : scale;
-        auto code = [&](float x) -> int {
-            return zero ? 0 : (int)fminf(fmaxf(roundf(x / scale), -qmax), qmax);
-        };
-        if (QBITS == 8) {
-            for (int e = lane; e < kv_dim; e += 64) {
-                const int h = e / d, j = e - h * d;
-                uint8_t *tile = pool + (blk * num_kv_heads + h) * tile_bytes;
-                const int64_t off = which ? (int64_t)j * block_size + t
-                                          : ((int64_t)(j / 8) * block_size + t) * 8 + j % 8;
-                tile[off] = (uint8_t)(int8_t)code(to_f32(src[e]));
-            }
-        } else {
-            for (int pe = lane; pe < kv_dim / 2; pe += 64) {
-                const int e = 2 * pe, h = e / d, j = e - h * d;
-                uint8_t *tile = pool + (blk * num_kv_heads + h) * tile_bytes;
-                const uint8_t byte = (uint8_t)((code(to_f32(src[e])) & 0x0f) |
-                                               ((code(to_f32(src[e + 1])) & 0x0f) << 4));
-                const int64_t off = which ? (int64_t)(j / 2) * block_size + t
-                                          : ((int64_t)(j / 8) * block_size + t) * 4 + (j % 8) / 2;
-                tile[off] = byte;
+        const float ok = scale > 0.f ? 1.f : 0.f;
+        if (lane == 0) (which ? v_scales : k_scales)[slot] = ok != 0.f ? scale : 0.f;
+#pragma unroll
+        for (int i = 0; i < NC; ++i) {
+            const int c = lane + 64 * i;
+            if (c >= nchunks) continue;
+            const int h = (8 * c) / d, j = 8 * c - h * d;
+            uint8_t *tile = pool + (blk * num_kv_heads + h) * tile_bytes;
+            int q[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q[k] = quant_code(x[i][k], ok, scale, qmax);
+            if constexpr (QBITS == 8) {
+                if (which == 0) {
+                    u32x2 w;
+                    w[0] = (q[0] & 0xff) | (q[1] & 0xff) << 8 | (q[2] & 0xff) << 16 | (uint32_t)(q[3] & 0xff) << 24;
+                    w[1] = (q[4] & 0xff) | (q[5] & 0xff) << 8 | (q[6] & 0xff) << 16 | (uint32_t)(q[7] & 0xff) << 24;
+                    *reinterpret_cast<u32x2 *>(tile + ((j / 8) * BS + t) * 8) = w;
+                } else {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) tile[(j + k) * BS + t] = (uint8_t)q[k];
+                }
+            } else {
+                uint8_t by[4];
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    by[m] = (uint8_t)((q[2 * m] & 0x0f) | (q[2 * m + 1] & 0x0f) << 4);
+                if (which == 0) {
+                    uint32_t w = by[0] | by[1] << 8 | by[2] << 16 | (uint32_t)by[3] << 24;
+                    *reinterpret_cast<uint32_t *>(tile + ((j / 8) * BS + t) * 4) = w;
+                } else {
+#pragma unroll
+                    for (int m = 0; m < 4; ++m) tile[(j / 2 + m) * BS + t] = by[m];
+                }
             }
         }
     }
@@ -192,15 +243,33 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
         return dlmk::fail(DLMK_ERR_UNSUPPORTED,
                           "dlmk_kv_append_quant: head_dim %d (multiple of 8) / block_size %d (16)",
                           head_dim, block_size);
+    const int64_t kv_dim = (int64_t)num_kv_heads * head_dim;
+    const int64_t chunks_per_lane = dlmk::ceil_div(kv_dim / 8, 64);
+    if (chunks_per_lane > 16)
+        return dlmk::fail(DLMK_ERR_UNSUPPORTED,
+                          "dlmk_kv_append_quant: kv_dim %lld above 8192", (long long)kv_dim);
+    if (reinterpret_cast<uintptr_t>(k_src) % 16 || reinterpret_cast<uintptr_t>(v_src) % 16)
+        return dlmk::fail(DLMK_ERR_INVALID_ARG,
+                          "dlmk_kv_append_quant: k_src / v_src not 16-byte aligned");
+    const int nc = chunks_per_lane <= 1 ? 1 : chunks_per_lane <= 2 ? 2 : chunks_per_lane <= 4 ? 4
+                 : chunks_per_lane <= 8 ? 8 : 16;
     const int64_t gx = dlmk::ceil_div(n_tok, 4);
     if (gx > 0x7fffffff) return dlmk::fail(DLMK_ERR_UNSUPPORTED, "dlmk_kv_append_quant: grid too large");
     auto s = (hipStream_t)stream;
     const int64_t num_slots = num_blocks * block_size;
     auto kp = (uint8_t *)k_pool, vp = (uint8_t *)v_pool;
-#define DLMK_LAUNCH(Q, S)                                                                       \
-    hipLaunchKernelGGL((kv_append_quant_kernel<Q, S>), dim3((unsigned)gx), dim3(256), 0, s, kp, vp, \
-                       k_scales, v_scales, (const S *)k_src, (const S *)v_src, slot_mapping,     \
-                       n_tok, num_kv_heads, head_dim, block_size, num_slots)
+#define DLMK_LAUNCH_NC(Q, S, NC)                                                                \
+    hipLaunchKernelGGL((kv_append_quant_kernel<Q, S, NC>), dim3((unsigned)gx), dim3(256), 0, s, kp, \
+                       vp, k_scales, v_scales, (const S *)k_src, (const S *)v_src, slot_mapping,  \
+                       n_tok, num_kv_heads, head_dim, num_slots)
+#define DLMK_LAUNCH(Q, S)                                             \
+    switch (nc) {                                                     \
+        case 1: DLMK_LAUNCH_NC(Q, S, 1); break;                       \
+        case 2: DLMK_LAUNCH_NC(Q, S, 2); break;                       \
+        case 4: DLMK_LAUNCH_NC(Q, S, 4); break;                       \
+        case 8: DLMK_LAUNCH_NC(Q, S, 8); break;                       \
+        default: DLMK_LAUNCH_NC(Q, S, 16); break;                     \
+    }
     const int q = quant == DLMK_I8 ? 8 : 4;
     switch (src_dtype * 16 + q) {
         case DLMK_F32 * 16 + 8: DLMK_LAUNCH(8, float); break;
@@ -213,6 +282,7 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
             return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_kv_append_quant: bad source dtype %d",
                               src_dtype);
     }
+#undef DLMK_LAUNCH_NC
 #undef DLMK_LAUNCH
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return dlmk::fail((int)e, "dlmk_kv_append_quant launch: %s", hipGetErrorString(e));

@@ -509,6 +509,15 @@ void orc_scatter_blocks(void *k_pool, void *v_pool, const void *staging, const i
 /* Per-token KV quantization: src/forward/cpu.rs:667-711.                    */
 /* ------------------------------------------------------------------------ */
 
+/* `(v / scale).round().clamp(-qmax, qmax) as i8` (:680, :696): round half
+ * away from zero, clamp, and Rust's saturating float->int cast, which sends NaN
+ * (from inf / inf, or a NaN element) to 0. */
+static int saturating_code(float r, float qmax) {
+    r = roundf(r);
+    if (r != r) return 0;
+    return (int)fminf(fmaxf(r, -qmax), qmax);
+}
+
 /* quantize_i8 (:667-680): scale = max|x| / 127; q = round(x/scale) clamped. */
 float orc_quantize_i8(const float *x, int64_t n, int8_t *q) {
     float mx = 0.0f;
@@ -518,10 +527,7 @@ float orc_quantize_i8(const float *x, int64_t n, int8_t *q) {
         memset(q, 0, n);
         return 0.0f;
     }
-    for (int64_t i = 0; i < n; ++i) {
-        float r = roundf(x[i] / scale);
-        q[i] = (int8_t)fminf(fmaxf(r, -127.0f), 127.0f);
-    }
+    for (int64_t i = 0; i < n; ++i) q[i] = (int8_t)saturating_code(x[i] / scale, 127.0f);
     return scale;
 }
 
@@ -534,7 +540,7 @@ float orc_quantize_i4(const float *x, int64_t n, uint8_t *packed) {
     float scale = mx / 7.0f;
     if (!(scale > 0.0f)) return 0.0f;
     for (int64_t i = 0; i < n; ++i) {
-        int8_t q = (int8_t)fminf(fmaxf(roundf(x[i] / scale), -7.0f), 7.0f);
+        int8_t q = (int8_t)saturating_code(x[i] / scale, 7.0f);
         uint8_t nib = (uint8_t)q & 0x0f;
         packed[i / 2] |= (i % 2 == 0) ? nib : (uint8_t)(nib << 4);
     }

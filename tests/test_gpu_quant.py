@@ -113,6 +113,8 @@ def test_kv_append_quant_bit_exact(oracle, torch_mod, ops, cuda, qname, src, Hkv
     v = tokens(rng, ntok, Hkv, d)
     k[3] = 0.0                            # all-zero token: scale 0, codes 0
     v[4] = 0.0
+    k[6, 0, 1] = np.nan                   # NaN element: skipped by the max, code 0
+    v[7, 0, 2] = np.inf                   # inf element: scale inf, every code 0
     kd, kf = src_dev(torch, k, src, cuda)
     vd, vf = src_dev(torch, v, src, cuda)
     kp, vp, ksc, vsc = garbage_pools(rng, oracle, nb, Hkv, d, quant)

@@ -257,6 +257,22 @@ def test_quantize_i4_round_trips_within_a_quantum(oracle):
     assert [oracle.read_i4(p2, 0, i) for i in range(3)] == [7.0, 1.0, -1.0]
 
 
+def test_quantize_nan_and_inf_follow_rust_casts(oracle):
+    """`(v / scale).round().clamp(..) as i8` (cpu.rs:680, :696): f32::max skips
+    NaN when taking max|x|, and the saturating cast sends NaN to 0, so a NaN
+    element gets code 0 and an inf element makes scale inf with every code 0
+    (finite / inf = 0, inf / inf = NaN -> 0)."""
+    x = np.array([np.nan, 1.0, -2.0, 0.0], np.float32)
+    q, s = oracle.quantize_i8(x)
+    assert s == np.float32(2.0) / np.float32(127.0)
+    assert q.tolist() == [0, 64, -127, 0]  # 1 / (2/127) = 63.5 -> 64 (half away from zero)
+    p4, s4 = oracle.quantize_i4(x)
+    assert [oracle.read_i4(p4, 0, i) for i in range(4)] == [0.0, 3.0, -7.0, 0.0]
+    for fn in (oracle.quantize_i8, oracle.quantize_i4):
+        codes, sc = fn(np.array([np.inf, 1.0, -np.inf], np.float32))
+        assert sc == np.inf and not codes.any()
+
+
 def test_bf16_decode_matches_torch(oracle):
     """The oracle's bf16 widening (used for bf16 pools) equals torch's bf16 -> f32."""
     import torch
