@@ -58,6 +58,10 @@ SIGNATURES = {
     "dlmk_cache_truncate_sequence": (_i32, [_vp, _u64, _u64]),
     "dlmk_cache_fork_sequence": (_i32, [_vp, _u64, _u64, _vp, _u32, C.POINTER(C.c_uint32),
                                         C.POINTER(KvExhaustedC)]),
+    "dlmk_cache_fork_sequence_shared": (_i32, [_vp, _u64, _u64]),
+    "dlmk_cache_append_tokens_cow": (_i32, [_vp, _u64, _u64, _vp, C.POINTER(C.c_uint32),
+                                            C.POINTER(KvExhaustedC)]),
+    "dlmk_cache_block_refcount": (_u32, [_vp, _u32]),
     "dlmk_cache_sequence_len": (_u64, [_vp, _u64]),
     "dlmk_cache_block_table": (_i64, [_vp, _u64, _vp, _u64]),
     "dlmk_cache_num_sequences": (_u64, [_vp]),

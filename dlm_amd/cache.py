@@ -182,6 +182,33 @@ class PagedKvCache:
         check(rc)
         return pairs[: n.value]
 
+    def fork_sequence_shared(self, src_seq: int, dst_seq: int) -> None:
+        """New sequence dst listing src's blocks (reference-counted, no copy):
+        the paged prefix cache.  Append to either with ``append_tokens_cow``."""
+        rc = lib().dlmk_cache_fork_sequence_shared(self._h, src_seq, dst_seq)
+        if rc == DLMK_ERR_UNKNOWN_SEQ:
+            raise UnknownSequence(rc, last_error())
+        check(rc)
+
+    def append_tokens_cow(self, seq_id: int, n: int) -> np.ndarray:
+        """append_tokens that first gives the sequence a private copy of a shared
+        partially-filled last block.  Returns the int32 [0 or 1, 2] (shared,
+        private) pair to hand to ``ops.copy_blocks`` before writing the tokens."""
+        pair = np.zeros((1, 2), np.int32)
+        n_pairs = C.c_uint32(0)
+        err = KvExhaustedC()
+        rc = lib().dlmk_cache_append_tokens_cow(self._h, seq_id, n,
+                                                pair.ctypes.data_as(C.c_void_p),
+                                                C.byref(n_pairs), C.byref(err))
+        if rc == DLMK_ERR_KV_EXHAUSTED:
+            raise KvCacheExhausted(err.requested, err.free, err.total)
+        check(rc)
+        return pair[: n_pairs.value]
+
+    def block_refcount(self, block: int) -> int:
+        """Number of block tables listing `block` (0 when free)."""
+        return lib().dlmk_cache_block_refcount(self._h, block)
+
     # -- queries (paged.rs:200-207)
     def sequence_len(self, seq_id: int) -> int:
         return lib().dlmk_cache_sequence_len(self._h, seq_id)

@@ -4,8 +4,17 @@
 // block ids, an ordered map of per-sequence {length, block table}, and an
 // append that checks capacity before committing anything.  Extensions for the
 // paged hot path: an injectable free order (seeded shuffled pools), truncate
-// (speculative rollback) and fork (prefix sharing by block copy), and the
-// device-side views (slot mappings, padded block tables).
+// (speculative rollback), fork by block copy (KvSnapshot clone) and fork by
+// shared blocks (prefix cache without copying), and the device-side views
+// (slot mappings, padded block tables).
+//
+// Shared blocks carry a reference count (one per table that lists them); a
+// block returns to the free list when its count drops to zero.  Only the
+// block holding position `length` can be written (appends go to the end), so
+// the one rule sharing needs is that a sequence never appends into a shared
+// partially-filled last block: dlmk_cache_append_tokens refuses that case and
+// dlmk_cache_append_tokens_cow first gives the sequence a private copy of the
+// block (returning the copy for the caller to run on the device).
 
 #include <cstring>
 #include <map>
@@ -19,6 +28,7 @@ struct dlmk_kv_cache {
     dlmk_kv_cache_config cfg;
     uint32_t total_blocks = 0;
     std::vector<uint32_t> free;  // top of stack = back()
+    std::vector<uint32_t> refs;  // per block: number of tables listing it (0 = free)
     struct Seq {
         uint64_t length = 0;
         std::vector<uint32_t> blocks;
@@ -34,11 +44,68 @@ dlmk_kv_cache_config normalized(const dlmk_kv_cache_config *cfg) {
     return c;
 }
 
+// Drop one reference to block b; a block nobody lists goes back on the stack.
+void release(dlmk_kv_cache *c, uint32_t b) {
+    if (--c->refs[b] == 0) c->free.push_back(b);
+}
+
+uint32_t take_free(dlmk_kv_cache *c) {
+    uint32_t b = c->free.back();
+    c->free.pop_back();
+    c->refs[b] = 1;
+    return b;
+}
+
+// True when the sequence's last block is partially filled and listed by
+// another table too: the next append would write into another sequence's
+// tokens' block.
+bool shared_partial_tail(const dlmk_kv_cache *c, const dlmk_kv_cache::Seq &s) {
+    return !s.blocks.empty() && s.length % c->cfg.block_size != 0 && c->refs[s.blocks.back()] > 1;
+}
+
 void set_exhausted(dlmk_kv_exhausted *err, uint64_t requested, uint32_t free, uint32_t total) {
     if (!err) return;
     err->requested = requested > 0xffffffffull ? 0xffffffffu : (uint32_t)requested;
     err->free = free;
     err->total = total;
+}
+
+// Append n tokens to seq_id; with cow, first replace a shared partial last
+// block by a private copy (pair = {shared, private}).  Capacity for both is
+// checked before anything changes (paged.rs:164-190: check, then commit).
+int append_impl(dlmk_kv_cache *c, uint64_t seq_id, uint64_t n, bool cow, int32_t *pair,
+                uint32_t *n_pairs, dlmk_kv_exhausted *err, const char *who) {
+    auto it = c->seqs.find(seq_id);
+    const bool exists = it != c->seqs.end();
+    uint64_t cur_len = exists ? it->second.length : 0;
+    uint64_t cur_blocks = exists ? it->second.blocks.size() : 0;
+    const bool must_copy = exists && n > 0 && shared_partial_tail(c, it->second);
+    if (must_copy && !cow)
+        return dlmk::fail(DLMK_ERR_INVALID_ARG,
+                          "%s: sequence %llu ends in a shared partially-filled block; append "
+                          "with dlmk_cache_append_tokens_cow", who, (unsigned long long)seq_id);
+    uint64_t new_len = cur_len + n;
+    uint64_t needed = dlmk_blocks_for_tokens(&c->cfg, new_len);
+    uint64_t to_alloc = (needed > cur_blocks ? needed - cur_blocks : 0) + (must_copy ? 1 : 0);
+    if (to_alloc > c->free.size()) {
+        set_exhausted(err, to_alloc, (uint32_t)c->free.size(), c->total_blocks);
+        return dlmk::fail(DLMK_ERR_KV_EXHAUSTED, "KV cache pool exhausted: need %llu more block(s), %u free of %u",
+                          (unsigned long long)to_alloc, (unsigned)c->free.size(), c->total_blocks);
+    }
+    auto &seq = c->seqs[seq_id];
+    if (n_pairs) *n_pairs = 0;
+    if (must_copy) {
+        const uint32_t shared = seq.blocks.back();
+        const uint32_t mine = take_free(c);
+        release(c, shared);  // still listed elsewhere: count stays >= 1
+        seq.blocks.back() = mine;
+        pair[0] = (int32_t)shared;
+        pair[1] = (int32_t)mine;
+        *n_pairs = 1;
+    }
+    while (seq.blocks.size() < needed) seq.blocks.push_back(take_free(c));
+    seq.length = new_len;
+    return DLMK_OK;
 }
 
 }  // namespace
@@ -72,6 +139,7 @@ dlmk_kv_cache *dlmk_cache_new(const dlmk_kv_cache_config *cfg, uint32_t total_bl
     // Low ids first: the stack holds n-1 ... 0 (paged.rs:118-119).
     c->free.resize(total_blocks);
     for (uint32_t i = 0; i < total_blocks; ++i) c->free[i] = total_blocks - 1 - i;
+    c->refs.assign(total_blocks, 0);
     return c;
 }
 
@@ -109,31 +177,22 @@ void dlmk_cache_destroy(dlmk_kv_cache *cache) { delete cache; }
 int dlmk_cache_append_tokens(dlmk_kv_cache *c, uint64_t seq_id, uint64_t n,
                              dlmk_kv_exhausted *err) {
     if (!c) return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_cache_append_tokens: null cache");
-    auto it = c->seqs.find(seq_id);
-    uint64_t cur_len = it == c->seqs.end() ? 0 : it->second.length;
-    uint64_t cur_blocks = it == c->seqs.end() ? 0 : it->second.blocks.size();
-    uint64_t new_len = cur_len + n;
-    uint64_t needed = dlmk_blocks_for_tokens(&c->cfg, new_len);
-    uint64_t to_alloc = needed > cur_blocks ? needed - cur_blocks : 0;
-    if (to_alloc > c->free.size()) {
-        set_exhausted(err, to_alloc, (uint32_t)c->free.size(), c->total_blocks);
-        return dlmk::fail(DLMK_ERR_KV_EXHAUSTED, "KV cache pool exhausted: need %llu more block(s), %u free of %u",
-                          (unsigned long long)to_alloc, (unsigned)c->free.size(), c->total_blocks);
-    }
-    auto &seq = c->seqs[seq_id];
-    for (uint64_t i = 0; i < to_alloc; ++i) {
-        seq.blocks.push_back(c->free.back());
-        c->free.pop_back();
-    }
-    seq.length = new_len;
-    return DLMK_OK;
+    return append_impl(c, seq_id, n, false, nullptr, nullptr, err, "dlmk_cache_append_tokens");
+}
+
+int dlmk_cache_append_tokens_cow(dlmk_kv_cache *c, uint64_t seq_id, uint64_t n,
+                                 int32_t *cow_pair, uint32_t *n_pairs, dlmk_kv_exhausted *err) {
+    if (!c || !cow_pair || !n_pairs)
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_cache_append_tokens_cow: null argument");
+    return append_impl(c, seq_id, n, true, cow_pair, n_pairs, err, "dlmk_cache_append_tokens_cow");
 }
 
 void dlmk_cache_free_sequence(dlmk_kv_cache *c, uint64_t seq_id) {
     if (!c) return;
     auto it = c->seqs.find(seq_id);
     if (it == c->seqs.end()) return;
-    c->free.insert(c->free.end(), it->second.blocks.begin(), it->second.blocks.end());
+    // Table order (paged.rs:195); shared blocks stay until their last table goes.
+    for (uint32_t b : it->second.blocks) release(c, b);
     c->seqs.erase(it);
 }
 
@@ -147,7 +206,7 @@ int dlmk_cache_truncate_sequence(dlmk_kv_cache *c, uint64_t seq_id, uint64_t new
     if (new_len >= seq.length) return DLMK_OK;
     uint64_t keep = dlmk_blocks_for_tokens(&c->cfg, new_len);
     while (seq.blocks.size() > keep) {
-        c->free.push_back(seq.blocks.back());
+        release(c, seq.blocks.back());
         seq.blocks.pop_back();
     }
     seq.length = new_len;
@@ -177,8 +236,7 @@ int dlmk_cache_fork_sequence(dlmk_kv_cache *c, uint64_t src_seq, uint64_t dst_se
     std::vector<uint32_t> src_blocks = it->second.blocks;
     auto &dst = c->seqs[dst_seq];
     for (uint64_t i = 0; i < need; ++i) {
-        uint32_t b = c->free.back();
-        c->free.pop_back();
+        uint32_t b = take_free(c);
         dst.blocks.push_back(b);
         pairs[2 * i] = (int32_t)src_blocks[i];
         pairs[2 * i + 1] = (int32_t)b;
@@ -186,6 +244,25 @@ int dlmk_cache_fork_sequence(dlmk_kv_cache *c, uint64_t src_seq, uint64_t dst_se
     dst.length = len;
     *n_pairs = (uint32_t)need;
     return DLMK_OK;
+}
+
+int dlmk_cache_fork_sequence_shared(dlmk_kv_cache *c, uint64_t src_seq, uint64_t dst_seq) {
+    if (!c) return dlmk::fail(DLMK_ERR_INVALID_ARG, "fork_shared: null cache");
+    auto it = c->seqs.find(src_seq);
+    if (it == c->seqs.end())
+        return dlmk::fail(DLMK_ERR_UNKNOWN_SEQ, "fork_shared: unknown source sequence %llu",
+                          (unsigned long long)src_seq);
+    if (c->seqs.count(dst_seq))
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "fork_shared: destination sequence %llu exists",
+                          (unsigned long long)dst_seq);
+    dlmk_kv_cache::Seq copy = it->second;
+    for (uint32_t b : copy.blocks) ++c->refs[b];
+    c->seqs.emplace(dst_seq, std::move(copy));
+    return DLMK_OK;
+}
+
+uint32_t dlmk_cache_block_refcount(const dlmk_kv_cache *c, uint32_t block) {
+    return c && block < c->total_blocks ? c->refs[block] : 0;
 }
 
 uint64_t dlmk_cache_sequence_len(const dlmk_kv_cache *c, uint64_t seq_id) {

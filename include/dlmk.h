@@ -111,10 +111,13 @@ dlmk_kv_cache *dlmk_cache_new_with_free_order(const dlmk_kv_cache_config *cfg,
 void dlmk_cache_destroy(dlmk_kv_cache *cache);
 
 /* append_tokens, paged.rs:164-190.  Atomic: on DLMK_ERR_KV_EXHAUSTED nothing
- * changes and *err (if non-NULL) holds {requested, free, total}. */
+ * changes and *err (if non-NULL) holds {requested, free, total}.  A sequence
+ * whose partially-filled last block is shared (dlmk_cache_fork_sequence_shared)
+ * gets DLMK_ERR_INVALID_ARG: append it with dlmk_cache_append_tokens_cow. */
 int dlmk_cache_append_tokens(dlmk_kv_cache *cache, uint64_t seq_id, uint64_t n,
                              dlmk_kv_exhausted *err);
-/* free_sequence, paged.rs:193-197 (blocks return in table order; no-op if unknown). */
+/* free_sequence, paged.rs:193-197 (blocks return in table order; no-op if
+ * unknown).  A shared block returns when the last table listing it goes. */
 void dlmk_cache_free_sequence(dlmk_kv_cache *cache, uint64_t seq_id);
 /* Extension: roll back to new_len tokens; freed tail blocks return last-first,
  * so re-appending pops the same blocks.  new_len >= len is a no-op. */
@@ -126,6 +129,23 @@ int dlmk_cache_fork_sequence(dlmk_kv_cache *cache, uint64_t src_seq, uint64_t ds
                              int32_t *pairs, uint32_t pairs_capacity, uint32_t *n_pairs,
                              dlmk_kv_exhausted *err);
 
+/* Extension, prefix sharing without copies (the paged form of dlm's prefix
+ * cache, which clones a KvSnapshot: src/batching.rs:32-72,
+ * src/forward/orchestrator.rs:73-105).  dst lists exactly src's blocks; each
+ * block's reference count grows by one and nothing is allocated or copied.
+ * Full blocks are never written again, so they stay shared for good; before
+ * either sequence appends into a shared partially-filled last block it must
+ * go through dlmk_cache_append_tokens_cow. */
+int dlmk_cache_fork_sequence_shared(dlmk_kv_cache *cache, uint64_t src_seq, uint64_t dst_seq);
+/* Extension: append_tokens that first replaces a shared partially-filled last
+ * block by a private block.  *n_pairs is 0 or 1; when 1, cow_pair (host
+ * int32[2]) = {shared block, private block}, to be copied with
+ * dlmk_copy_blocks before the sequence's new tokens are written.  Capacity for
+ * the copy and the new blocks is checked first (atomic, as append_tokens). */
+int dlmk_cache_append_tokens_cow(dlmk_kv_cache *cache, uint64_t seq_id, uint64_t n,
+                                 int32_t *cow_pair, uint32_t *n_pairs, dlmk_kv_exhausted *err);
+/* Number of block tables listing `block` (0: free or out of range). */
+uint32_t dlmk_cache_block_refcount(const dlmk_kv_cache *cache, uint32_t block);
 /* sequence_len, paged.rs:200-202 (0 if unknown). */
 uint64_t dlmk_cache_sequence_len(const dlmk_kv_cache *cache, uint64_t seq_id);
 /* block_table, paged.rs:205-207: copies up to cap ids into out (may be NULL)

@@ -65,6 +65,30 @@ class Mirror:
                            to_dev(t, slots, self.cuda), num_kv_heads=HKV, head_dim=D)
         self.oracle.paged_append(self.kh, self.vh, k, v, slots, HKV, D, BS)
 
+    def append_cow(self, seq_tokens, sigma=0.5):
+        """append with copy-on-write of shared partial tails: books for every
+        sequence, one block-copy launch for the copies they hand out, then the
+        tokens (the copies run first on the stream)."""
+        pairs, work = [], []
+        for s, n in seq_tokens:
+            start = self.cache.sequence_len(s)
+            pairs.append(self.cache.append_tokens_cow(s, n))
+            work.append((s, start, n))
+        pairs = np.concatenate(pairs).astype(np.int32) if pairs else np.zeros((0, 2), np.int32)
+        if len(pairs):
+            self.ops.copy_blocks(self.kd, self.vd, to_dev(self.torch, pairs, self.cuda),
+                                 self.block_bytes)
+            self.oracle.copy_blocks(self.kh, self.vh, pairs, self.block_bytes)
+        slots = np.concatenate([self.cache.slot_mapping(s, st, n) for s, st, n in work])
+        n = len(slots)
+        k = (self.rng.standard_normal((n, HKV, D)) * sigma).astype(np.float16)
+        v = (self.rng.standard_normal((n, HKV, D)) * sigma).astype(np.float16)
+        t = self.torch
+        self.ops.kv_append(self.kd, self.vd, to_dev(t, k, self.cuda), to_dev(t, v, self.cuda),
+                           to_dev(t, slots, self.cuda), num_kv_heads=HKV, head_dim=D)
+        self.oracle.paged_append(self.kh, self.vh, k, v, slots, HKV, D, BS)
+        return pairs
+
     def attention(self, seqs, nq=1, check=None, max_blocks=None):
         """Device attention for seqs; oracle check on the index subset `check`."""
         max_blocks = max_blocks or max(len(self.cache.block_table(s)) for s in seqs)
@@ -222,4 +246,42 @@ def test_config5_verify_rollback_fork_swap(oracle, torch_mod, cuda):
     m.kd[ids_dev.long()] = 0  # evicted blocks are reused by someone else meanwhile
     m.vd[ids_dev.long()] = 0
     m_ops.swap_in(m.kd, m.vd, host, ids_dev, m.block_bytes, staging)
+    m.assert_pools_equal()
+
+
+def test_prefix_cache_on_shared_blocks(oracle, torch_mod, cuda):
+    """dlm's prefix cache (src/batching.rs:32-72: a prompt's KvSnapshot cloned
+    for every request that extends it) on shared blocks: a 1000-token system
+    prompt is prefilled once and forked to 6 requests by reference; every
+    sequence appends its own suffix (copy-on-write of the shared partial block)
+    and then decodes.  Pools stay bit-identical to the mirror, attention matches
+    the oracle for every sequence, and the prompt's full blocks are stored once."""
+    banner("prefix cache on shared blocks")
+    m = Mirror(torch_mod, cuda, oracle, 3000, seed=9)
+    rng = np.random.default_rng(99)
+    prefix, n_req = 1000, 6
+    m.append([(0, prefix)])
+    for r in range(1, n_req + 1):
+        m.cache.fork_sequence_shared(0, r)
+    seqs = list(range(n_req + 1))
+    used = m.cache.stats().used_blocks
+    assert used == -(-prefix // BS)  # forks allocate nothing
+    pairs = m.append_cow([(s, int(rng.integers(1, 300))) for s in seqs])
+    # The shared partial block (8 tokens) is copied for every sequence but the
+    # last one to append, which keeps it; the 62 full blocks stay shared.
+    assert len(pairs) == n_req
+    full = prefix // BS
+    prompt_blocks = m.cache.block_table(n_req)[:full]
+    for s in seqs:
+        assert m.cache.block_table(s)[:full] == prompt_blocks
+    assert all(m.cache.block_refcount(b) == n_req + 1 for b in prompt_blocks)
+    m.assert_pools_equal()
+    m.attention(seqs)
+    for _ in range(4):  # decode steps: private tails now, so no copies
+        assert len(m.append_cow([(s, 1) for s in seqs])) == 0
+        m.attention(seqs)
+    m.cache.free_sequence(0)  # the origin finishes: the prompt stays for the others
+    assert all(m.cache.block_refcount(b) == n_req for b in prompt_blocks)
+    assert not set(prompt_blocks) & set(m.cache.free_list())
+    m.attention(seqs[1:])
     m.assert_pools_equal()
