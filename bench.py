@@ -87,6 +87,10 @@ def parse():
                    help="time one phase only (for profiling runs)")
     p.add_argument("--cpu-seconds", type=float, default=10.0,
                    help="bound on the CPU baseline sample's work")
+    p.add_argument("--traffic", default="pmc", choices=["pmc", "off"],
+                   help="pmc: measure the attention launch's HBM bytes with rocprofv3 --pmc "
+                        "(FETCH_SIZE and WRITE_SIZE passes over this script, scaled by the "
+                        "same counters on --copy-calibration) before the timed run")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run dlmk_copy_blocks over 4096 pairs of 32-KiB blocks in each of 2 "
                         "pools (256 MiB read + 256 MiB written per launch), to scale "
@@ -122,6 +126,64 @@ def append_bytes(w, n_tok):
     """Per appended token: K+V read, K+V stored (codes and scale when
     quantized), and an 8-byte slot."""
     return n_tok * (2 * (w.hkv * w.d * elem_bytes(w) + kv_token_bytes(w)) + 8)
+
+
+def _pmc_pass(counter, script_args, timeout_s=120):
+    """One rocprofv3 --pmc pass (a single counter, no tracing domains) over this
+    script as a child process; returns {kernel name: mean counter value per
+    dispatch}.  The child runs alone: this process has not touched the GPU."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+    prof = shutil.which("rocprofv3")
+    if prof is None:
+        raise RuntimeError("rocprofv3 not on PATH")
+    out = tempfile.mkdtemp(prefix="dlmk_pmc_")
+    cmd = ["timeout", "-s", "KILL", str(timeout_s), prof, "--pmc", counter, "--output-format", "csv",
+           "-d", out, "-o", "run", "--", sys.executable, os.path.abspath(__file__), *script_args]
+    res = subprocess.run(cmd, capture_output=True, text=True, cwd=tempfile.gettempdir())
+    if res.returncode != 0:
+        raise RuntimeError(f"rocprofv3 --pmc {counter} exited {res.returncode}: {res.stderr[-300:]}")
+    sums, counts = {}, {}
+    for root, _, files in os.walk(out):
+        for f in files:
+            if not f.endswith("counter_collection.csv"):
+                continue
+            with open(os.path.join(root, f)) as fh:
+                for row in csv.DictReader(fh):
+                    if row.get("Counter_Name") != counter:
+                        continue
+                    k = row["Kernel_Name"]
+                    sums[k] = sums.get(k, 0.0) + float(row["Counter_Value"])
+                    counts[k] = counts.get(k, 0) + 1
+    shutil.rmtree(out, ignore_errors=True)
+    if not sums:
+        raise RuntimeError(f"no {counter} rows in rocprofv3 output")
+    return {k: sums[k] / counts[k] for k in sums}
+
+
+def measure_traffic(args):
+    """HBM bytes per attention launch (partition + combine kernels): FETCH_SIZE
+    and WRITE_SIZE (KiB per dispatch) from their own --pmc passes over
+    `--only attention`, each scaled by what the same counter reads for the copy
+    calibration kernel, whose bytes are known.  Returns (bytes, detail)."""
+    base = ["--workload", args.workload, "--kv-quant", args.kv_quant, "--only", "attention",
+            "--steps", "20", "--warmup", "20", "--no-cpu-baseline", "--traffic", "off"]
+    cal = ["--copy-calibration", "--steps", "20", "--traffic", "off"]
+    known = 2 * 4096 * 8 * BS * 128 * 2  # bytes read (and written) per copy launch
+    detail = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        print(f"[bench] rocprofv3 --pmc {counter} passes", file=sys.stderr, flush=True)
+        attn = _pmc_pass(counter, base)
+        copy = _pmc_pass(counter, cal)
+        kib = sum(v for k, v in attn.items() if "paged_attn" in k)
+        ckib = sum(v for k, v in copy.items() if "copy_blocks" in k)
+        scale = known / (ckib * 1024)
+        detail[counter] = {"kib_per_launch": round(kib, 1), "copy_kib_per_launch": round(ckib, 1),
+                           "scale": round(scale, 4), "bytes_per_launch": int(kib * 1024 * scale)}
+    total = detail["FETCH_SIZE"]["bytes_per_launch"] + detail["WRITE_SIZE"]["bytes_per_launch"]
+    return total, detail
 
 
 def copy_calibration(torch, ops, steps):
@@ -237,6 +299,14 @@ def main():
                                    "GPU and multi-GPU runs are out of scope for this path",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+
+    traffic, traffic_note = None, None
+    if args.traffic == "pmc" and not args.copy_calibration and args.only is None:
+        # Before this process touches the GPU: the counter passes run as children.
+        try:
+            traffic, traffic_note = measure_traffic(args)
+        except Exception as e:  # the timed line stands without it
+            traffic_note = f"not measured: {e}"
 
     import torch
     from dlm_amd import KvCacheConfig, PagedKvCache, ops
@@ -433,8 +503,9 @@ def main():
                      "dlmk_paged_decode_attention"),
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
-            "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": None,
+            "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
             "kernel": "paged_attn_mfma_kernel" if w.dtype != "f32" else "paged_attn_valu_kernel",
+            "traffic_detail": traffic_note,
         },
     }
     if "fork" in w.extras:

@@ -212,6 +212,31 @@ def test_paged_attention_is_deterministic_and_order_free(torch_mod, ops, cuda):
     assert np.array_equal(c, a[perm])
 
 
+def test_paged_attention_workspace_reuse_across_shapes(oracle, torch_mod, ops, cuda):
+    """One workspace serves calls of different shapes back to back, twice over:
+    nothing a call leaves in it disturbs the next call."""
+    torch = torch_mod
+    banner("attention workspace reuse across shapes")
+    rng = np.random.default_rng(31)
+    shapes = [([4000, 3100], 64, 8, 1), ([600, 1300, 40, 2500] * 3, 32, 8, 1),
+              ([4, 1030, 2100, 700], 32, 8, 4), ([300, 1200], 32, 2, 1)]
+    loads = [make_workload(rng, ctx, Hq, Hkv, 128, np.float16, nq=nq, sigma=0.5)
+             for ctx, Hq, Hkv, nq in shapes]
+    need = max(ops.attention_workspace_bytes(len(w.ctx), w.nq, w.Hq, w.d, w.tables.shape[1])
+               for w in loads)
+    ws = ops.alloc_workspace(need, cuda)
+    for rep in range(2):
+        for w in loads:
+            out = ops.paged_decode_attention(
+                to_dev(torch, w.q, cuda), to_dev(torch, w.k_pool, cuda),
+                to_dev(torch, w.v_pool, cuda), to_dev(torch, w.tables, cuda),
+                to_dev(torch, w.ctx, cuda), num_kv_heads=w.Hkv, scale=float(w.scale),
+                out_dtype=torch.float32, workspace=ws)
+            torch.cuda.synchronize()
+            assert_close(out.cpu().numpy(), oracle_attention(oracle, w), F16_ATOL, F16_RTOL,
+                         f"rep {rep} B={len(w.ctx)} Hq={w.Hq} nq={w.nq}")
+
+
 def test_paged_attention_unsupported_shape_raises(torch_mod, ops, cuda):
     torch = torch_mod
     from dlm_amd import DlmkError
