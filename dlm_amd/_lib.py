@@ -71,6 +71,9 @@ SIGNATURES = {
     "dlmk_cache_fill_block_tables": (_i32, [_vp, _vp, _u32, _u32, _vp, _vp]),
     "dlmk_kv_append": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _i64, _i32, _i32, _i32, _i64, _i32]),
     "dlmk_paged_attention_workspace_size": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
+    "dlmk_decode_block_workspace_size": (_sz, [_i32] * 7),
+    "dlmk_decode_block_paged": (_i32, [_vp] + [_i32] * 7 + [_f32, _i32, _i32] + [_vp] * 14 +
+                                [_vp, _vp, _i64, _vp, _i32, _i32, _i32, _vp, _sz]),
     "dlmk_paged_decode_attention": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _i32,
                                            _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _vp,
                                            _sz]),

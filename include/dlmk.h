@@ -44,6 +44,14 @@ extern "C" {
  * quantized pool formats (dlm's KvQuant::Int8 / Int4, src/forward/cpu.rs:627-639). */
 enum dlmk_dtype { DLMK_F32 = 0, DLMK_F16 = 1, DLMK_BF16 = 2, DLMK_I8 = 3, DLMK_I4 = 4 };
 
+/* Projection weight dtypes of dlmk_decode_block_paged: dlm's DLM_W_* tags
+ * (src/gpu/kernels.cu:61-65, Weights::dtype_code at src/forward/cpu.rs:307-317),
+ * same values.  INT4 / INT8 are dlm's group-affine blobs: codes (int4 two a
+ * byte, low nibble first), padded to 4 bytes, then ceil(n / group) f32 scales,
+ * then as many f32 zero-points; element = (code - zero) * scale (QuantLayout,
+ * src/forward/cpu.rs:132-159). */
+enum dlmk_wdtype { DLMK_W_F32 = 0, DLMK_W_BF16 = 1, DLMK_W_F16 = 2, DLMK_W_INT4 = 3, DLMK_W_INT8 = 4 };
+
 /* Negative status codes (positive values are hipError_t). */
 #define DLMK_OK 0
 #define DLMK_ERR_INVALID_ARG -1 /* DlmError::ShapeMismatch / InvalidConfig analogue */
@@ -288,6 +296,40 @@ int dlmk_swap_out(void *stream, void *host_buf, const void *k_pool, const void *
 int dlmk_swap_in(void *stream, void *k_pool, void *v_pool, const void *host_buf,
                  const int32_t *block_ids, int64_t n, size_t block_bytes, int64_t num_blocks,
                  void *dev_staging, size_t staging_bytes);
+
+/* One decode block over the paged cache: replaces dlm_decode_block
+ * (src/gpu/kernels.cu:313-392, declared at src/forward/gpu.rs:34-64; the CPU
+ * oracle is decode_block, src/forward/cpu.rs:1156-1219).  Same arguments in
+ * the same order, with three changes:
+ *   - kv_keys / kv_values (one contiguous f32 history per kernel) become this
+ *     layer's f32 pools k_pool [num_blocks][num_kv_heads][head_dim/4][16][4]
+ *     and v_pool [num_blocks][num_kv_heads][head_dim][16], addressed through
+ *     the sequence's device block table (int32 [max_blocks_per_seq]);
+ *   - an explicit stream, first, instead of the default stream;
+ *   - a caller-owned workspace (dlmk_decode_block_workspace_size bytes,
+ *     256-byte aligned) instead of thread_local scratch (kernels.cu:283-306).
+ * The new token's K (after RoPE) and V go to position num_positions
+ * (block block_table[num_positions / 16], offset num_positions % 16; those
+ * blocks must already be the sequence's, as PagedKvCache::append_tokens
+ * leaves them); attention covers positions 0..num_positions.  x [hidden] is
+ * updated in place.  q/k/v_bias may be NULL; inv_freq [head_dim/2] is the
+ * host-computed rope_inv_freqs (src/forward/cpu.rs:1057-1092).  Weight rows
+ * are read 16 bytes at a time: hidden_size, q_dim, inter and (int4/int8) the
+ * group size must be multiples of 4 (f32), 8 (bf16, f16), 32 (int4) or 16
+ * (int8) elements, else DLMK_ERR_UNSUPPORTED; head_dim must be 64 or 128 and
+ * num_heads / num_kv_heads 1, 2, 4 or 8 (the f32 paged attention kernels).
+ * Returns 0 or an error code; never synchronises. */
+size_t dlmk_decode_block_workspace_size(int hidden_size, int q_dim, int kv_dim, int num_heads,
+                                        int head_dim, int inter, int max_blocks_per_seq);
+int dlmk_decode_block_paged(
+    void *stream, int hidden_size, int q_dim, int kv_dim, int num_heads, int num_kv_heads,
+    int head_dim, int inter, float rms_eps, int w_dtype, int w_group_size, const void *q_proj,
+    const void *k_proj, const void *v_proj, const void *o_proj, const void *gate_proj,
+    const void *up_proj, const void *down_proj, const float *in_norm, const float *post_norm,
+    const float *q_bias, const float *k_bias, const float *v_bias, const float *inv_freq,
+    float *x, void *k_pool, void *v_pool, int64_t num_blocks, const int32_t *block_table,
+    int max_blocks_per_seq, int num_positions, int position, void *workspace,
+    size_t workspace_bytes);
 
 /* Pinned host memory, PinnedBuffer (src/memory/pinned.rs:38-112) analogue. */
 int dlmk_alloc_pinned(void **ptr, size_t bytes);

@@ -740,3 +740,224 @@ void orc_paged_attention_quant(float *out, const float *q, const void *k_pool, c
         free(vs);
     }
 }
+
+/* ======================================================================== */
+/* One decode block (the caller of the paged path): decode_block,           */
+/* src/forward/cpu.rs:1156-1219, with its KvLayerCache replaced by a paged  */
+/* f32 pool and a block table.                                              */
+/* ======================================================================== */
+
+#define ORC_W_F32 0
+#define ORC_W_BF16 1
+#define ORC_W_F16 2
+#define ORC_W_INT4 3
+#define ORC_W_INT8 4
+
+/* QuantLayout (src/forward/cpu.rs:132-159): [codes][pad to 4][scales g x f32]
+ * [zeros g x f32], g = ceil(n / group_size). */
+typedef struct {
+    int64_t scales_off, zeros_off, num_groups, total_bytes;
+} orc_qlayout;
+
+static orc_qlayout qlayout(int dtype, int64_t n, int64_t group_size) {
+    orc_qlayout L;
+    int64_t code_bytes = dtype == ORC_W_INT4 ? (n + 1) / 2 : n;
+    L.scales_off = (code_bytes + 3) / 4 * 4;
+    L.num_groups = (n + (group_size > 0 ? group_size : 1) - 1) / (group_size > 0 ? group_size : 1);
+    L.zeros_off = L.scales_off + L.num_groups * 4;
+    L.total_bytes = L.zeros_off + L.num_groups * 4;
+    return L;
+}
+
+int64_t orc_quant_blob_bytes(int dtype, int64_t n, int64_t group_size) {
+    return qlayout(dtype, n, group_size).total_bytes;
+}
+
+static float blob_f32(const uint8_t *blob, int64_t off) {
+    float f;
+    memcpy(&f, blob + off, 4);
+    return f;
+}
+
+/* Weights::get (src/forward/cpu.rs:204-217): element i as f32.  bf16 is the
+ * high half of an f32 (:171-174); f16 via the exact decoder above; int4 /
+ * int8 per int4_get / int8_get (:321-347): (code - zero) * scale of the
+ * element's group, codes low-nibble-first. */
+float orc_weight_get(const void *w, int dtype, int64_t n, int64_t group_size, int64_t i) {
+    const uint8_t *b = (const uint8_t *)w;
+    switch (dtype) {
+        case ORC_W_F32: return ((const float *)w)[i];
+        case ORC_W_BF16: return bf16_to_f32(((const uint16_t *)w)[i]);
+        case ORC_W_F16: return orc_f16_to_f32(((const uint16_t *)w)[i]);
+        default: {
+            orc_qlayout L = qlayout(dtype, n, group_size);
+            float code = dtype == ORC_W_INT4 ? (float)((i % 2 == 0) ? (b[i / 2] & 0x0F) : (b[i / 2] >> 4))
+                                             : (float)b[i];
+            int64_t g = i / group_size;
+            return (code - blob_f32(b, L.zeros_off + g * 4)) * blob_f32(b, L.scales_off + g * 4);
+        }
+    }
+}
+
+/* quantize_groups (src/quant/dequant.rs:200-236) packed into the blob layout
+ * by Weights::quantize_int4 / quantize_int8 (src/forward/cpu.rs:237-305):
+ * per group, scale = (max - min) / levels (1 when max - min < f32::EPSILON),
+ * zero = -min / scale, code = round((v - min) / scale) clamped to [0, levels]
+ * (f32::round: half away from zero, C roundf).  blob must hold
+ * orc_quant_blob_bytes(dtype, n, group_size) bytes. */
+int orc_quantize_weights(const float *values, int64_t n, int64_t group_size, int dtype,
+                         uint8_t *blob) {
+    if (group_size <= 0 || (dtype != ORC_W_INT4 && dtype != ORC_W_INT8)) return ORC_ERR_INVALID;
+    orc_qlayout L = qlayout(dtype, n, group_size);
+    float levels = dtype == ORC_W_INT4 ? 15.0f : 255.0f;
+    memset(blob, 0, (size_t)L.total_bytes);
+    for (int64_t g = 0; g < L.num_groups; ++g) {
+        int64_t start = g * group_size, end = start + group_size < n ? start + group_size : n;
+        float mn = INFINITY, mx = -INFINITY;
+        for (int64_t i = start; i < end; ++i) {
+            mn = fminf(mn, values[i]);
+            mx = fmaxf(mx, values[i]);
+        }
+        float scale = fabsf(mx - mn) < 1.1920929e-7f ? 1.0f : (mx - mn) / levels;
+        float zero = -mn / scale;
+        for (int64_t i = start; i < end; ++i) {
+            float c = roundf((values[i] - mn) / scale);
+            c = c < 0.0f ? 0.0f : (c > levels ? levels : c);
+            uint8_t code = (uint8_t)c;
+            if (dtype == ORC_W_INT8)
+                blob[i] = code;
+            else
+                blob[i / 2] |= (uint8_t)((code & 0x0F) << (i % 2 ? 4 : 0));
+        }
+        memcpy(blob + L.scales_off + g * 4, &scale, 4);
+        memcpy(blob + L.zeros_off + g * 4, &zero, 4);
+    }
+    return ORC_OK;
+}
+
+/* matvec / matvec_native (src/forward/cpu.rs:852-903): y[o] is the sequential
+ * f32 sum over j of get(o * in_dim + j) * x[j] (Iterator::sum).  `n` is the
+ * matrix's element count, for the quantized layouts. */
+void orc_matvec(const void *w, int dtype, int64_t group_size, const float *x, int64_t out_dim,
+                int64_t in_dim, float *y) {
+    int64_t n = out_dim * in_dim;
+    for (int64_t o = 0; o < out_dim; ++o) {
+        float s = 0.0f;
+        for (int64_t j = 0; j < in_dim; ++j)
+            s += orc_weight_get(w, dtype, n, group_size, o * in_dim + j) * x[j];
+        y[o] = s;
+    }
+}
+
+/* rmsnorm (src/forward/cpu.rs:934-943): mean of squares (sequential sum / n),
+ * inv = 1 / sqrt(mean + eps), out = v * inv * w. */
+void orc_rmsnorm(const float *x, const float *w, int64_t n, float eps, float *out) {
+    float ss = 0.0f;
+    for (int64_t i = 0; i < n; ++i) ss += x[i] * x[i];
+    float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int64_t i = 0; i < n; ++i) out[i] = x[i] * inv * w[i];
+}
+
+/* silu (src/forward/cpu.rs:960-962). */
+float orc_silu(float x) { return x / (1.0f + expf(-x)); }
+
+/* rope_inv_freqs (src/forward/cpu.rs:1057-1092).  scaling: 0 none, 1 linear
+ * (factor), 2 llama3 (factor, low_freq_factor, high_freq_factor,
+ * original_max_position). */
+void orc_rope_inv_freqs(int head_dim, float theta, int scaling, float factor, float low_ff,
+                        float high_ff, float orig_max, float *out) {
+    for (int i = 0; i < head_dim / 2; ++i) {
+        float base = powf(theta, -2.0f * (float)i / (float)head_dim);
+        float f = base;
+        if (scaling == 1) {
+            f = base / factor;
+        } else if (scaling == 2) {
+            float wavelen = 2.0f * 3.14159265358979323846f / base;
+            float low_wavelen = orig_max / low_ff, high_wavelen = orig_max / high_ff;
+            if (wavelen > low_wavelen) {
+                f = base / factor;
+            } else if (wavelen < high_wavelen) {
+                f = base;
+            } else {
+                float smooth = (orig_max / wavelen - low_ff) / (high_ff - low_ff);
+                f = (1.0f - smooth) * base / factor + smooth * base;
+            }
+        }
+        out[i] = f;
+    }
+}
+
+/* rope_inplace (src/forward/cpu.rs:1094-1114): NeoX split-half rotation of
+ * each head's (i, i + d/2) pair by position * inv_freq[i]. */
+void orc_rope(float *v, int num_heads, int head_dim, int64_t position, const float *inv_freq) {
+    int half = head_dim / 2;
+    for (int h = 0; h < num_heads; ++h) {
+        int64_t base = (int64_t)h * head_dim;
+        for (int i = 0; i < half; ++i) {
+            float angle = (float)position * inv_freq[i];
+            float s = sinf(angle), c = cosf(angle);
+            float a = v[base + i], b = v[base + i + half];
+            v[base + i] = a * c - b * s;
+            v[base + i + half] = a * s + b * c;
+        }
+    }
+}
+
+typedef struct {
+    int hidden_size, num_heads, num_kv_heads, head_dim, inter;
+    float rms_eps;
+    int w_dtype;
+    int64_t w_group_size;
+} orc_block_config;
+
+/* decode_block (src/forward/cpu.rs:1156-1219), dense SwiGLU FFN, with the KV
+ * history in a paged f32 pool: the token goes to position num_positions of
+ * the sequence (slot table[p / bs] * bs + p % bs), then attention runs over
+ * positions 0..num_positions through the table.  Biases may be NULL.  x is
+ * the hidden state, updated in place. */
+int orc_decode_block_paged(const orc_block_config *c, const void *q_proj, const void *k_proj,
+                           const void *v_proj, const void *o_proj, const void *gate_proj,
+                           const void *up_proj, const void *down_proj, const float *in_norm,
+                           const float *post_norm, const float *q_bias, const float *k_bias,
+                           const float *v_bias, const float *inv_freq, float *x, void *k_pool,
+                           void *v_pool, const int32_t *table, int max_blocks, int64_t num_blocks,
+                           int bs, int64_t num_positions, int64_t position) {
+    int H = c->hidden_size, Hq = c->num_heads, Hkv = c->num_kv_heads, d = c->head_dim;
+    int qd = Hq * d, kvd = Hkv * d, I = c->inter, dt = c->w_dtype;
+    int64_t gs = c->w_group_size;
+    if ((num_positions + 1 + bs - 1) / bs > max_blocks) return ORC_ERR_INVALID;
+    float *normed = malloc(sizeof(float) * H), *q = malloc(sizeof(float) * qd);
+    float *k = malloc(sizeof(float) * kvd), *v = malloc(sizeof(float) * kvd);
+    float *ctx = malloc(sizeof(float) * qd), *attn = malloc(sizeof(float) * H);
+    float *gate = malloc(sizeof(float) * I), *up = malloc(sizeof(float) * I);
+    float *down = malloc(sizeof(float) * H);
+
+    orc_rmsnorm(x, in_norm, H, c->rms_eps, normed);
+    orc_matvec(q_proj, dt, gs, normed, qd, H, q);
+    orc_matvec(k_proj, dt, gs, normed, kvd, H, k);
+    orc_matvec(v_proj, dt, gs, normed, kvd, H, v);
+    if (q_bias) for (int i = 0; i < qd; ++i) q[i] += q_bias[i];
+    if (k_bias) for (int i = 0; i < kvd; ++i) k[i] += k_bias[i];
+    if (v_bias) for (int i = 0; i < kvd; ++i) v[i] += v_bias[i];
+    orc_rope(q, Hq, d, position, inv_freq);
+    orc_rope(k, Hkv, d, position, inv_freq);
+
+    int64_t slot = (int64_t)table[num_positions / bs] * bs + num_positions % bs;
+    orc_paged_append(k_pool, v_pool, k, v, &slot, 1, Hkv, d, bs, ORC_F32, num_blocks);
+    int32_t ctx_len = (int32_t)(num_positions + 1);
+    orc_paged_attention(ctx, q, k_pool, v_pool, ORC_F32, table, &ctx_len, 1, 1, Hq, Hkv, d, bs,
+                        max_blocks, 1.0f / sqrtf((float)d));
+    orc_matvec(o_proj, dt, gs, ctx, H, qd, attn);
+    for (int i = 0; i < H; ++i) x[i] = x[i] + attn[i];
+
+    orc_rmsnorm(x, post_norm, H, c->rms_eps, normed);
+    orc_matvec(gate_proj, dt, gs, normed, I, H, gate);
+    orc_matvec(up_proj, dt, gs, normed, I, H, up);
+    for (int i = 0; i < I; ++i) gate[i] = orc_silu(gate[i]) * up[i];
+    orc_matvec(down_proj, dt, gs, gate, H, I, down);
+    for (int i = 0; i < H; ++i) x[i] += down[i];
+
+    free(normed); free(q); free(k); free(v); free(ctx); free(attn);
+    free(gate); free(up); free(down);
+    return ORC_OK;
+}

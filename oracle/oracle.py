@@ -49,6 +49,12 @@ class CacheConfig(C.Structure):
                 ("head_dim", C.c_uint32), ("block_size", C.c_uint32)]
 
 
+class BlockConfigC(C.Structure):
+    _fields_ = [("hidden_size", C.c_int), ("num_heads", C.c_int), ("num_kv_heads", C.c_int),
+                ("head_dim", C.c_int), ("inter", C.c_int), ("rms_eps", C.c_float),
+                ("w_dtype", C.c_int), ("w_group_size", C.c_int64)]
+
+
 def _p(a):
     return a.ctypes.data_as(C.c_void_p) if a is not None else None
 
@@ -99,6 +105,18 @@ def _declare(L):
         "orc_paged_attention_quant": (None, [vp, vp, vp, vp, vp, vp, i32, vp, vp, i32, i32, i32,
                                              i32, i32, i32, i32, f32]),
     }
+    sig.update({
+        "orc_quant_blob_bytes": (i64, [i32, i64, i64]),
+        "orc_weight_get": (f32, [vp, i32, i64, i64, i64]),
+        "orc_quantize_weights": (i32, [vp, i64, i64, i32, vp]),
+        "orc_matvec": (None, [vp, i32, i64, vp, i64, i64, vp]),
+        "orc_rmsnorm": (None, [vp, vp, i64, f32, vp]),
+        "orc_silu": (f32, [f32]),
+        "orc_rope_inv_freqs": (None, [i32, f32, i32, f32, f32, f32, f32, vp]),
+        "orc_rope": (None, [vp, i32, i32, i64, vp]),
+        "orc_decode_block_paged": (i32, [C.POINTER(BlockConfigC)] + [vp] * 14 +
+                                   [vp, vp, vp, i32, i64, i32, i64, i64]),
+    })
     for name, (res, args) in sig.items():
         fn = getattr(L, name)
         fn.restype = res
@@ -405,3 +423,89 @@ def paged_attention_quant(q, k_pool, v_pool, k_scales, v_scales, quant, tables, 
                                     _p(v_scales), quant, _p(tables), _p(ctx_lens), len(ctx_lens),
                                     nq, Hq, Hkv, d, bs, tables.shape[1], float(scale))
     return out
+
+
+# ---------------------------------------------------------------- decode block
+
+W_F32, W_BF16, W_F16, W_INT4, W_INT8 = 0, 1, 2, 3, 4
+QUANT_GROUP_SIZE = 128  # src/forward/cpu.rs:161
+
+
+def quant_blob_bytes(w_dtype, n, group_size=QUANT_GROUP_SIZE) -> int:
+    return lib().orc_quant_blob_bytes(w_dtype, n, group_size)
+
+
+def quantize_weights(values, w_dtype, group_size=QUANT_GROUP_SIZE) -> np.ndarray:
+    """Weights::quantize_int4 / quantize_int8 blob (codes, pad, scales, zeros)."""
+    v = np.ascontiguousarray(values, np.float32).ravel()
+    blob = np.zeros(quant_blob_bytes(w_dtype, v.size, group_size), np.uint8)
+    rc = lib().orc_quantize_weights(_p(v), v.size, group_size, w_dtype, _p(blob))
+    if rc != 0:
+        raise ValueError("bad quantization arguments")
+    return blob
+
+
+def weight_get(w, w_dtype, n, i, group_size=QUANT_GROUP_SIZE) -> float:
+    return lib().orc_weight_get(_p(np.ascontiguousarray(w)), w_dtype, n, group_size, i)
+
+
+def matvec(w, w_dtype, x, out_dim, in_dim, group_size=QUANT_GROUP_SIZE) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    y = np.zeros(out_dim, np.float32)
+    lib().orc_matvec(_p(np.ascontiguousarray(w)), w_dtype, group_size, _p(x), out_dim, in_dim,
+                     _p(y))
+    return y
+
+
+def rmsnorm(x, w, eps) -> np.ndarray:
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.zeros_like(x)
+    lib().orc_rmsnorm(_p(x), _p(np.ascontiguousarray(w, np.float32)), x.size, eps, _p(out))
+    return out
+
+
+def silu(x: float) -> float:
+    return lib().orc_silu(x)
+
+
+def rope_inv_freqs(head_dim, theta, scaling=None) -> np.ndarray:
+    """scaling: None, ("linear", factor) or ("llama3", factor, low, high, original_max)."""
+    out = np.zeros(head_dim // 2, np.float32)
+    kind, args = 0, (1.0, 1.0, 1.0, 1.0)
+    if scaling is not None and scaling[0] == "linear":
+        kind, args = 1, (scaling[1], 1.0, 1.0, 1.0)
+    elif scaling is not None:
+        kind, args = 2, tuple(scaling[1:5])
+    lib().orc_rope_inv_freqs(head_dim, theta, kind, *args, _p(out))
+    return out
+
+
+def rope(v, num_heads, head_dim, position, inv_freq) -> np.ndarray:
+    v = np.array(v, np.float32)
+    lib().orc_rope(_p(v), num_heads, head_dim, position,
+                   _p(np.ascontiguousarray(inv_freq, np.float32)))
+    return v
+
+
+def decode_block_paged(cfg, weights, x, k_pool, v_pool, table, num_positions, position,
+                       inv_freq, bs=16):
+    """decode_block over a paged f32 pool (pools updated in place); returns the new hidden.
+
+    cfg: dict with hidden_size, num_heads, num_kv_heads, head_dim, inter, rms_eps, w_dtype,
+    w_group_size.  weights: dict q_proj k_proj v_proj o_proj gate_proj up_proj down_proj
+    in_norm post_norm and optional q_bias k_bias v_bias."""
+    c = BlockConfigC(cfg["hidden_size"], cfg["num_heads"], cfg["num_kv_heads"], cfg["head_dim"],
+                     cfg["inter"], cfg["rms_eps"], cfg["w_dtype"], cfg.get("w_group_size", 0))
+    x = np.array(x, np.float32)
+    table = np.ascontiguousarray(table, np.int32)
+    names = ["q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj",
+             "in_norm", "post_norm", "q_bias", "k_bias", "v_bias"]
+    ptrs = [_p(np.ascontiguousarray(weights[n])) if weights.get(n) is not None else None
+            for n in names]
+    num_blocks = k_pool.shape[0]
+    rc = lib().orc_decode_block_paged(C.byref(c), *ptrs, _p(np.ascontiguousarray(inv_freq,
+                                      np.float32)), _p(x), _p(k_pool), _p(v_pool), _p(table),
+                                      table.size, num_blocks, bs, num_positions, position)
+    if rc != 0:
+        raise ValueError("decode_block_paged: table too short")
+    return x
