@@ -78,7 +78,9 @@ def parse():
     p.add_argument("--steps", type=int, default=200, help="timed steps (rounded to a multiple of 20)")
     p.add_argument("--warmup", type=int, default=500,
                    help="untimed steps run before each timed region (lets clocks settle)")
-    p.add_argument("--workload", default="config2", choices=sorted(WORKLOADS))
+    p.add_argument("--workload", default="config2", choices=sorted(WORKLOADS) + ["block8b"],
+                   help="block8b: dlmk_decode_block_paged on Llama-3-8B layers (the caller "
+                        "of the paged path; a design-notes line, not the headline metric)")
     p.add_argument("--kv-quant", default="none", choices=["none", "int8", "int4"],
                    help="store K/V as per-token-scaled int8/int4 codes (dlm's --kv-quant); "
                         "queries and new tokens stay f16")
@@ -184,6 +186,91 @@ def measure_traffic(args):
                            "scale": round(scale, 4), "bytes_per_launch": int(kib * 1024 * scale)}
     total = detail["FETCH_SIZE"]["bytes_per_launch"] + detail["WRITE_SIZE"]["bytes_per_launch"]
     return total, detail
+
+
+def bench_block(args):
+    """One decode token through two Llama-3-8B layers (hidden 4096, 32/8 heads,
+    head_dim 128, inter 14336) with bf16 weights, f32 paged KV (dlm's KV dtype)
+    and a 2048-token history on shuffled blocks, via dlmk_decode_block_paged.
+    Two layers with distinct weights (2 x 436 MB, above the 256 MB Infinity
+    Cache) so every token streams its weights from HBM.  Timed as HIP-graph
+    replays of 10 tokens.  Bytes per token: weights + the KV the attention
+    reads + the appended K/V."""
+    import torch
+    from dlm_amd.block import BlockConfig, LayerWeights, PagedGpuKernel
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(SEED)
+    H, Hq, Hkv, d, I, L, ctx = 4096, 32, 8, 128, 14336, 2, 2048
+    cfg = BlockConfig(H, Hq, Hkv, d, I, rope_theta=500000.0, rms_eps=1e-5,
+                      rope_scaling=("llama3", 8.0, 1.0, 4.0, 8192.0))
+
+    def mat(o, i):
+        w = torch.empty((o, i), dtype=torch.bfloat16, device=dev)
+        w.uniform_(-0.02, 0.02, generator=gen)
+        return w.view(torch.uint8).reshape(-1)
+
+    layers = [LayerWeights(mat(cfg.q_dim, H), mat(cfg.kv_dim, H), mat(cfg.kv_dim, H),
+                           mat(H, cfg.q_dim), mat(I, H), mat(I, H), mat(H, I),
+                           torch.ones(H, device=dev), torch.ones(H, device=dev))
+              for _ in range(L)]
+    nblk = -(-(ctx + 1) // BS)
+    max_blocks = 256
+    kern = PagedGpuKernel(cfg, layers, 1, max_blocks_per_seq=max_blocks, device=dev)
+    num_pool = 4 * nblk
+    pools = [(torch.randn((num_pool, Hkv, d * BS), generator=gen, device=dev) * 0.5,
+              torch.randn((num_pool, Hkv, d * BS), generator=gen, device=dev) * 0.5)
+             for _ in range(L)]
+    rng = np.random.default_rng(SEED)
+    table = np.zeros(max_blocks, np.int32)
+    table[:nblk] = rng.permutation(num_pool)[:nblk]
+    table_d = torch.from_numpy(table).to(dev)
+    x = torch.randn(H, generator=gen, device=dev)
+
+    def token():
+        for layer in range(L):
+            kern.run_block(layer, x, pools[layer], table_d, ctx, ctx)
+            x.mul_(0.5)  # keep the residual stream bounded across replays
+
+    for _ in range(3):
+        token()
+    torch.cuda.synchronize()
+    reps = 10
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(reps):
+            token()
+    for _ in range(max(1, args.warmup // 50)):
+        g.replay()
+    torch.cuda.synchronize()
+    n = max(2, args.steps // reps)
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(n):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    ms_token = a.elapsed_time(b) / (n * reps)
+    wbytes = 2 * (cfg.q_dim * H + 2 * cfg.kv_dim * H + H * cfg.q_dim + 3 * I * H)
+    kvbytes = (ctx + 1) * 2 * cfg.kv_dim * 4
+    tok_bytes = L * (wbytes + kvbytes + 2 * cfg.kv_dim * 4)
+    gbps = tok_bytes / (ms_token * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "paged decode block HBM GB/s (Llama-3-8B layers, bf16 weights, f32 paged KV)",
+        "value": round(gbps, 1), "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+        "ms_per_token": round(ms_token, 5), "us_per_layer": round(ms_token * 1e3 / L, 2),
+        "tokens_per_s": round(1e3 / ms_token, 1), "dtype": "bf16 weights, f32 KV and math",
+        "data": "synthetic (uniform(-0.02, 0.02) weights, N(0,1)*0.5 KV, seeded)",
+        "config": {"workload": "dlmk_decode_block_paged, 2 Llama-3-8B layers, ctx 2048",
+                   "hidden": H, "heads": Hq, "kv_heads": Hkv, "head_dim": d, "inter": I,
+                   "layers": L, "context": ctx},
+        "algorithmic_bytes_per_token": tok_bytes,
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
+                     "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4)},
+        "timing": f"HIP events around replays of a HIP graph of {reps} tokens",
+    }), flush=True)
 
 
 def copy_calibration(torch, ops, steps):
@@ -300,6 +387,9 @@ def main():
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
+    if args.workload == "block8b":
+        bench_block(args)
+        return
     traffic, traffic_note = None, None
     if args.traffic == "pmc" and not args.copy_calibration and args.only is None:
         # Before this process touches the GPU: the counter passes run as children.
