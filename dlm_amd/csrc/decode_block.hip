@@ -11,11 +11,13 @@
 // registers, as the reference's load_w<> does.
 //
 // Kernels (all HBM-bound on the weights at decode batch 1):
-//   rmsnorm_kernel       one 1024-thread work-group.
-//   gemv_kernel          x staged once per work-group in LDS as f32; one wave
-//                        per output row, 16-byte weight loads, 8 in flight per
-//                        lane, wave reduction; epilogue = bias store, residual
-//                        add, or (two matrices) SwiGLU.
+//   gemv_kernel          x staged once per work-group in LDS as f32 (both
+//                        rmsnorms are folded into that staging); a grid of
+//                        resident work-groups; one wave per output row,
+//                        16-byte weight loads, 16 in flight per lane (8 per
+//                        matrix for SwiGLU), wave reduction; epilogue = bias
+//                        store, residual add, or (two matrices) SwiGLU; q, k
+//                        and v as one launch.
 //   rope_append_kernel   RoPE on q and k (NeoX split-half, host-computed
 //                        inv_freq), then the new token's K and V straight into
 //                        the pools at the slot the block table gives; also
@@ -51,28 +53,6 @@ __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int o = 1; o < W; o <<= 1) v += __shfl_xor(v, o);
     return v;
-}
-
-// ---------------------------------------------------------------------------
-// rmsnorm (src/forward/cpu.rs:934-943): out = x * (1 / sqrt(mean(x^2) + eps)) * w.
-// ---------------------------------------------------------------------------
-constexpr int kNormThreads = 1024;
-
-__global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float *__restrict__ x,
-                                                               const float *__restrict__ w,
-                                                               float *__restrict__ out, int n,
-                                                               float eps) {
-    __shared__ float part[kNormThreads / 64];
-    float ss = 0.f;
-    for (int i = threadIdx.x; i < n; i += kNormThreads) ss += x[i] * x[i];
-    ss = wave_sum<64>(ss);
-    if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    float tot = 0.f;
-#pragma unroll
-    for (int i = 0; i < kNormThreads / 64; ++i) tot += part[i];
-    const float inv = 1.0f / sqrtf(tot / (float)n + eps);
-    for (int i = threadIdx.x; i < n; i += kNormThreads) out[i] = x[i] * inv * w[i];
 }
 
 // ---------------------------------------------------------------------------
@@ -189,59 +169,146 @@ __host__ __device__ inline QOffsets qoffsets(int dt, int64_t n, int64_t gs) {
 
 enum Epilogue { kStoreBias = 0, kAddInto = 1, kSwiGLU = 2 };
 
-// out_dim rows of a row-major [out_dim][in_dim] matrix W (and, for SwiGLU, of
-// a second matrix W2) times x.  Work-group: kGemvWaves waves; x is staged in
-// LDS once; wave w of work-group b takes rows (b * kGemvWaves + w) +
-// k * gridDim.x * kGemvWaves.  Epilogues: kStoreBias out[o] = dot (+ bias[o]);
-// kAddInto out[o] += dot (the residual); kSwiGLU out[o] = silu(dot) * dot2.
-template <int DT, int EPI>
-__global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(
-    const uint8_t *__restrict__ W, const uint8_t *__restrict__ W2, const float *__restrict__ x,
-    const float *__restrict__ bias, float *__restrict__ out, int out_dim, int in_dim, int gs) {
+// Up to three matrices over the same input, as one launch (q, k and v share
+// the normalised hidden state).  A segment's rows follow the previous
+// segment's in the launch's row numbering.
+struct GemvSeg {
+    const uint8_t *W, *W2;  // W2: the up projection of the SwiGLU epilogue
+    const float *bias;      // kStoreBias: may be null
+    float *out;
+    int rows;
+};
+
+struct GemvArgs {
+    GemvSeg seg[3];
+    int nseg, total_rows, in_dim, gs;
+    const float *x;
+    const float *norm_w;  // non-null: x is staged as rmsnorm(x) * norm_w
+    float eps;
+};
+
+// Row-major [rows][in_dim] matrices times x.  Work-group: kGemvWaves waves
+// and x staged once in LDS as f32 -- normalised on the way when norm_w is set
+// (rmsnorm, src/forward/cpu.rs:934-943: every work-group sums the squares in
+// the same order, so all see the same factor).  Wave w of work-group b takes
+// launch rows b * kGemvWaves + w + k * gridDim.x * kGemvWaves, so a grid of
+// resident work-groups amortises the staging over several rows.  One row per
+// wave at a time: 16-byte weight loads, U in flight per lane, a wave
+// reduction.  Epilogues: kStoreBias out[o] = dot (+ bias[o]); kAddInto
+// out[o] += dot (the residual); kSwiGLU out[o] = silu(dot(W)) * dot(W2).
+template <int DT, int EPI, int RW, int U>
+__global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     using C = WChunk<DT>;
     constexpr int E = C::E;
     extern __shared__ float xs[];
-    for (int i = threadIdx.x; i < in_dim; i += 64 * kGemvWaves) xs[i] = x[i];
+    __shared__ float red[kGemvWaves];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int in_dim = a.in_dim;
+    // Stage x with 16-byte loads, kStageUnroll in flight per thread (in_dim is
+    // a multiple of 4: every weight dtype reads at least 4 elements a chunk),
+    // summing the squares on the way; then normalise in place.
+    constexpr int kStageUnroll = 8;
+    const int n4 = in_dim / 4;
+    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
+    float4 *xs4 = reinterpret_cast<float4 *>(xs);
+    float ss = 0.f;
+    for (int i0 = 0; i0 < n4; i0 += 64 * kGemvWaves * kStageUnroll) {
+        float4 v[kStageUnroll];
+#pragma unroll
+        for (int u = 0; u < kStageUnroll; ++u) {
+            const int i = i0 + u * 64 * kGemvWaves + threadIdx.x;
+            v[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int u = 0; u < kStageUnroll; ++u) {
+            const int i = i0 + u * 64 * kGemvWaves + threadIdx.x;
+            if (i < n4) {
+                xs4[i] = v[u];
+                ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
+            }
+        }
+    }
+    if (a.norm_w != nullptr) {
+        ss = wave_sum<64>(ss);
+        if (lane == 0) red[wave] = ss;
+        __syncthreads();
+        float tot = 0.f;
+#pragma unroll
+        for (int w = 0; w < kGemvWaves; ++w) tot += red[w];
+        const float inv = 1.0f / sqrtf(tot / (float)in_dim + a.eps);
+        for (int i = threadIdx.x; i < in_dim; i += 64 * kGemvWaves)
+            xs[i] = xs[i] * inv * a.norm_w[i];
+    }
     __syncthreads();
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int64_t n = (int64_t)out_dim * in_dim;
-    const QOffsets qo = qoffsets(DT, n, gs);
     const int chunks = in_dim / E;
     const int64_t row_bytes = (int64_t)in_dim * 16 / E;
-    for (int o = blockIdx.x * kGemvWaves + wave; o < out_dim; o += gridDim.x * kGemvWaves) {
-        const u32x4 *wr = reinterpret_cast<const u32x4 *>(W + o * row_bytes);
-        const u32x4 *wr2 = EPI == kSwiGLU ? reinterpret_cast<const u32x4 *>(W2 + o * row_bytes)
-                                          : nullptr;
-        float s = 0.f, s2 = 0.f;
-        for (int c0 = 0; c0 < chunks; c0 += 64 * kGemvUnroll) {
-            u32x4 r[kGemvUnroll], r2[kGemvUnroll];
+    // RW rows per wave at a time, U chunk loads per lane per row per step:
+    // RW * U (x2 for SwiGLU) 16-byte loads in flight whatever the row length.
+    for (int r0 = (blockIdx.x * kGemvWaves + wave) * RW; r0 < a.total_rows;
+         r0 += gridDim.x * kGemvWaves * RW) {
+        GemvSeg g[RW];
+        int o[RW];
+        QOffsets qo[RW];
 #pragma unroll
-            for (int u = 0; u < kGemvUnroll; ++u) {
+        for (int j = 0; j < RW; ++j) {
+            // Segment of launch row r0 + j (explicit selects: a dynamically
+            // indexed kernel-argument array would be copied to scratch).  Rows
+            // past the end repeat the last row, and are not stored.
+            int rr = min(r0 + j, a.total_rows - 1);
+            g[j] = a.seg[0];
+            if (a.nseg > 1 && rr >= a.seg[0].rows) {
+                rr -= a.seg[0].rows;
+                g[j] = a.seg[1];
+                if (a.nseg > 2 && rr >= a.seg[1].rows) {
+                    rr -= a.seg[1].rows;
+                    g[j] = a.seg[2];
+                }
+            }
+            o[j] = rr;
+            qo[j] = qoffsets(DT, (int64_t)g[j].rows * in_dim, a.gs);
+        }
+        float acc[RW], acc2[RW];
+#pragma unroll
+        for (int j = 0; j < RW; ++j) acc[j] = acc2[j] = 0.f;
+        for (int c0 = 0; c0 < chunks; c0 += 64 * U) {
+            u32x4 w1[RW][U], w2[RW][U];
+#pragma unroll
+            for (int u = 0; u < U; ++u) {
                 const int c = min(c0 + u * 64 + lane, chunks - 1);
-                r[u] = stream_load(wr + c);
-                if constexpr (EPI == kSwiGLU) r2[u] = stream_load(wr2 + c);
+#pragma unroll
+                for (int j = 0; j < RW; ++j) {
+                    w1[j][u] = stream_load(reinterpret_cast<const u32x4 *>(g[j].W + o[j] * row_bytes) + c);
+                    if constexpr (EPI == kSwiGLU)
+                        w2[j][u] = stream_load(reinterpret_cast<const u32x4 *>(g[j].W2 + o[j] * row_bytes) + c);
+                }
             }
 #pragma unroll
-            for (int u = 0; u < kGemvUnroll; ++u) {
+            for (int u = 0; u < U; ++u) {
                 const int c = c0 + u * 64 + lane;
                 if (c < chunks) {
-                    const int64_t i0 = (int64_t)o * in_dim + (int64_t)c * E;
-                    s += C::dot(r[u], xs + c * E, W, qo.scales, qo.zeros, gs, i0);
-                    if constexpr (EPI == kSwiGLU)
-                        s2 += C::dot(r2[u], xs + c * E, W2, qo.scales, qo.zeros, gs, i0);
+#pragma unroll
+                    for (int j = 0; j < RW; ++j) {
+                        const int64_t i0 = (int64_t)o[j] * in_dim + (int64_t)c * E;
+                        acc[j] += C::dot(w1[j][u], xs + c * E, g[j].W, qo[j].scales, qo[j].zeros, a.gs, i0);
+                        if constexpr (EPI == kSwiGLU)
+                            acc2[j] += C::dot(w2[j][u], xs + c * E, g[j].W2, qo[j].scales, qo[j].zeros, a.gs, i0);
+                    }
                 }
             }
         }
-        s = wave_sum<64>(s);
-        if constexpr (EPI == kSwiGLU) s2 = wave_sum<64>(s2);
-        if (lane == 0) {
-            if constexpr (EPI == kStoreBias) {
-                out[o] = s + (bias ? bias[o] : 0.f);
-            } else if constexpr (EPI == kAddInto) {
-                out[o] = out[o] + s;
-            } else {
-                out[o] = s / (1.0f + expf(-s)) * s2;  // silu(gate) * up, src/forward/cpu.rs:960-975
+#pragma unroll
+        for (int j = 0; j < RW; ++j) {
+            const float s1 = wave_sum<64>(acc[j]);
+            const float s2 = EPI == kSwiGLU ? wave_sum<64>(acc2[j]) : 0.f;
+            if (lane == 0 && r0 + j < a.total_rows) {
+                if constexpr (EPI == kStoreBias) {
+                    g[j].out[o[j]] = s1 + (g[j].bias ? g[j].bias[o[j]] : 0.f);
+                } else if constexpr (EPI == kAddInto) {
+                    g[j].out[o[j]] = g[j].out[o[j]] + s1;
+                } else {
+                    g[j].out[o[j]] = s1 / (1.0f + expf(-s1)) * s2;  // silu(gate) * up, cpu.rs:960-975
+                }
             }
         }
     }
@@ -303,50 +370,98 @@ int w_elems_per_chunk(int dt) {
     }
 }
 
-int gemv_grid(int out_dim) {
-    return std::max(1, std::min((out_dim + kGemvWaves - 1) / kGemvWaves, 1024));
+int device_cus() {
+    static int cus[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    if (cus[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c < 1)
+            c = 1;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
+// Resident work-groups: as many per compute unit as the LDS of the staged x
+// (and a cap of 8) allows, so that every work-group is running from the start
+// and each stages x once for all its rows.
+// Resident work-groups only (the occupancy of this instantiation with its
+// LDS), so every work-group runs from the start and stages x once for all
+// its rows.
+template <int DT, int EPI, int RW, int U>
+void launch_gemv_rw(hipStream_t st, const GemvArgs &a) {
+    const auto kernel = gemv_kernel<DT, EPI, RW, U>;
+    const size_t lds = (size_t)a.in_dim * sizeof(float);
+    int per_cu = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64 * kGemvWaves, lds) !=
+            hipSuccess || per_cu < 1)
+        per_cu = 1;
+    const int want = (a.total_rows + kGemvWaves * RW - 1) / (kGemvWaves * RW);
+    const int grid = std::max(1, std::min(want, device_cus() * per_cu));
+    hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kGemvWaves), lds, st, a);
+}
+
+// About 16 weight loads in flight per lane (8 per matrix for SwiGLU): rows of
+// at least 16 (8) loads per lane run one at a time, shorter rows 2 or 4 at once.
+template <int DT, int EPI>
+void launch_gemv_epi(hipStream_t st, const GemvArgs &a) {
+    constexpr int T = EPI == kSwiGLU ? 8 : 16;
+    const int per_lane = (a.in_dim / WChunk<DT>::E + 63) / 64;  // chunk loads per lane per row
+    if (per_lane >= T)
+        launch_gemv_rw<DT, EPI, 1, T>(st, a);
+    else if (per_lane >= T / 2)
+        launch_gemv_rw<DT, EPI, 2, T / 2>(st, a);
+    else
+        launch_gemv_rw<DT, EPI, 4, T / 4>(st, a);
 }
 
 template <int DT>
-void launch_gemv(int epi, hipStream_t st, const void *W, const void *W2, const float *x,
-                 const float *bias, float *out, int out_dim, int in_dim, int gs) {
-    const size_t lds = (size_t)in_dim * sizeof(float);
-    const auto *w = static_cast<const uint8_t *>(W);
-    const auto *w2 = static_cast<const uint8_t *>(W2);
-    const dim3 grid(gemv_grid(out_dim)), block(64 * kGemvWaves);
+void launch_gemv(int epi, hipStream_t st, const GemvArgs &a) {
     if (epi == kStoreBias)
-        hipLaunchKernelGGL((gemv_kernel<DT, kStoreBias>), grid, block, lds, st, w, w2, x, bias, out,
-                           out_dim, in_dim, gs);
+        launch_gemv_epi<DT, kStoreBias>(st, a);
     else if (epi == kAddInto)
-        hipLaunchKernelGGL((gemv_kernel<DT, kAddInto>), grid, block, lds, st, w, w2, x, bias, out,
-                           out_dim, in_dim, gs);
+        launch_gemv_epi<DT, kAddInto>(st, a);
     else
-        hipLaunchKernelGGL((gemv_kernel<DT, kSwiGLU>), grid, block, lds, st, w, w2, x, bias, out,
-                           out_dim, in_dim, gs);
+        launch_gemv_epi<DT, kSwiGLU>(st, a);
 }
 
-void gemv(int dt, int epi, hipStream_t st, const void *W, const void *W2, const float *x,
-          const float *bias, float *out, int out_dim, int in_dim, int gs) {
+void gemv(int dt, int epi, hipStream_t st, const GemvArgs &a) {
     switch (dt) {
-        case DLMK_W_F32: launch_gemv<DLMK_W_F32>(epi, st, W, W2, x, bias, out, out_dim, in_dim, gs); break;
-        case DLMK_W_BF16: launch_gemv<DLMK_W_BF16>(epi, st, W, W2, x, bias, out, out_dim, in_dim, gs); break;
-        case DLMK_W_F16: launch_gemv<DLMK_W_F16>(epi, st, W, W2, x, bias, out, out_dim, in_dim, gs); break;
-        case DLMK_W_INT4: launch_gemv<DLMK_W_INT4>(epi, st, W, W2, x, bias, out, out_dim, in_dim, gs); break;
-        default: launch_gemv<DLMK_W_INT8>(epi, st, W, W2, x, bias, out, out_dim, in_dim, gs); break;
+        case DLMK_W_F32: launch_gemv<DLMK_W_F32>(epi, st, a); break;
+        case DLMK_W_BF16: launch_gemv<DLMK_W_BF16>(epi, st, a); break;
+        case DLMK_W_F16: launch_gemv<DLMK_W_F16>(epi, st, a); break;
+        case DLMK_W_INT4: launch_gemv<DLMK_W_INT4>(epi, st, a); break;
+        default: launch_gemv<DLMK_W_INT8>(epi, st, a); break;
     }
 }
 
-// Workspace regions, each on a 256-byte boundary: normed[H], q[qd], k[kvd],
-// v[kvd], ctx[qd], act[inter], ctx_len (int32), then the attention workspace.
+GemvArgs gemv_args(const float *x, int in_dim, int gs, const float *norm_w, float eps) {
+    GemvArgs a{};
+    a.x = x;
+    a.in_dim = in_dim;
+    a.gs = gs;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    return a;
+}
+
+void add_seg(GemvArgs &a, const void *W, const void *W2, const float *bias, float *out, int rows) {
+    a.seg[a.nseg++] = GemvSeg{static_cast<const uint8_t *>(W), static_cast<const uint8_t *>(W2),
+                              bias, out, rows};
+    a.total_rows += rows;
+}
+
+// Workspace regions, each on a 256-byte boundary: q[qd], k[kvd], v[kvd],
+// ctx[qd], act[inter], ctx_len (int32), then the attention workspace.
 struct BlockWs {
-    int64_t normed, q, k, v, ctx, act, ctx_len, attn, total;
+    int64_t q, k, v, ctx, act, ctx_len, attn, total;
 };
 
-BlockWs block_ws(int H, int qd, int kvd, int inter, int64_t attn_bytes) {
+BlockWs block_ws(int qd, int kvd, int inter, int64_t attn_bytes) {
     const auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
     BlockWs w;
-    w.normed = 0;
-    w.q = up(w.normed + 4LL * H);
+    w.q = 0;
     w.k = up(w.q + 4LL * qd);
     w.v = up(w.k + 4LL * kvd);
     w.ctx = up(w.v + 4LL * kvd);
@@ -368,7 +483,7 @@ size_t dlmk_decode_block_workspace_size(int hidden_size, int q_dim, int kv_dim, 
         return 0;
     const size_t attn = dlmk_paged_attention_workspace_size(1, 1, num_heads, head_dim, kBlock,
                                                             max_blocks_per_seq);
-    return (size_t)block_ws(hidden_size, q_dim, kv_dim, inter, (int64_t)attn).total;
+    return (size_t)block_ws(q_dim, kv_dim, inter, (int64_t)attn).total;
 }
 
 int dlmk_decode_block_paged(
@@ -405,7 +520,7 @@ int dlmk_decode_block_paged(
                           (long long)(lds_max / 4));
     const size_t attn_need = dlmk_paged_attention_workspace_size(1, 1, num_heads, head_dim, kBlock,
                                                                  max_blocks_per_seq);
-    const BlockWs ws = block_ws(hidden_size, q_dim, kv_dim, inter, (int64_t)attn_need);
+    const BlockWs ws = block_ws(q_dim, kv_dim, inter, (int64_t)attn_need);
     if (!workspace || (int64_t)workspace_bytes < ws.total)
         return dlmk::fail(DLMK_ERR_WORKSPACE, "%s: workspace %zu bytes, need %lld", who,
                           workspace_bytes, (long long)ws.total);
@@ -414,7 +529,6 @@ int dlmk_decode_block_paged(
 
     hipStream_t st = static_cast<hipStream_t>(stream);
     char *base = static_cast<char *>(workspace);
-    float *normed = reinterpret_cast<float *>(base + ws.normed);
     float *q = reinterpret_cast<float *>(base + ws.q);
     float *k = reinterpret_cast<float *>(base + ws.k);
     float *v = reinterpret_cast<float *>(base + ws.v);
@@ -423,12 +537,12 @@ int dlmk_decode_block_paged(
     int32_t *ctx_len = reinterpret_cast<int32_t *>(base + ws.ctx_len);
     const int gs = quant ? w_group_size : 0;
 
-    // Attention sublayer.
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, st, x, in_norm, normed,
-                       hidden_size, rms_eps);
-    gemv(w_dtype, kStoreBias, st, q_proj, nullptr, normed, q_bias, q, q_dim, hidden_size, gs);
-    gemv(w_dtype, kStoreBias, st, k_proj, nullptr, normed, k_bias, k, kv_dim, hidden_size, gs);
-    gemv(w_dtype, kStoreBias, st, v_proj, nullptr, normed, v_bias, v, kv_dim, hidden_size, gs);
+    // Attention sublayer: rmsnorm folded into the q/k/v launch's staging.
+    GemvArgs qkv = gemv_args(x, hidden_size, gs, in_norm, rms_eps);
+    add_seg(qkv, q_proj, nullptr, q_bias, q, q_dim);
+    add_seg(qkv, k_proj, nullptr, k_bias, k, kv_dim);
+    add_seg(qkv, v_proj, nullptr, v_bias, v, kv_dim);
+    gemv(w_dtype, kStoreBias, st, qkv);
     const int rope_threads = (num_heads + num_kv_heads) * (head_dim / 2) + kv_dim;
     hipLaunchKernelGGL(rope_append_kernel, dim3((rope_threads + 255) / 256), dim3(256), 0, st, q,
                        k, v, inv_freq, static_cast<float *>(k_pool), static_cast<float *>(v_pool),
@@ -441,13 +555,18 @@ int dlmk_decode_block_paged(
         num_kv_heads, head_dim, kBlock, max_blocks_per_seq, num_blocks,
         1.0f / sqrtf((float)head_dim), attn_need ? base + ws.attn : nullptr, attn_need);
     if (rc != DLMK_OK) return rc;
-    gemv(w_dtype, kAddInto, st, o_proj, nullptr, ctx, nullptr, x, hidden_size, q_dim, gs);
+    GemvArgs oproj = gemv_args(ctx, q_dim, gs, nullptr, 0.f);
+    add_seg(oproj, o_proj, nullptr, nullptr, x, hidden_size);
+    gemv(w_dtype, kAddInto, st, oproj);
 
-    // MLP sublayer (SwiGLU).
-    hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kNormThreads), 0, st, x, post_norm, normed,
-                       hidden_size, rms_eps);
-    gemv(w_dtype, kSwiGLU, st, gate_proj, up_proj, normed, nullptr, act, inter, hidden_size, gs);
-    gemv(w_dtype, kAddInto, st, down_proj, nullptr, act, nullptr, x, hidden_size, inter, gs);
+    // MLP sublayer (SwiGLU): the post-attention rmsnorm folded into the
+    // gate/up launch's staging.
+    GemvArgs gu = gemv_args(x, hidden_size, gs, post_norm, rms_eps);
+    add_seg(gu, gate_proj, up_proj, nullptr, act, inter);
+    gemv(w_dtype, kSwiGLU, st, gu);
+    GemvArgs down = gemv_args(act, inter, gs, nullptr, 0.f);
+    add_seg(down, down_proj, nullptr, nullptr, x, hidden_size);
+    gemv(w_dtype, kAddInto, st, down);
     e = hipGetLastError();
     if (e != hipSuccess) return dlmk::fail((int)e, "%s launch: %s", who, hipGetErrorString(e));
     return DLMK_OK;

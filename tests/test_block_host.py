@@ -23,13 +23,13 @@ def test_block_config_geometry():
 
 
 def test_decode_block_workspace_size(dlmk):
-    # regions: normed, q, k, v, ctx, act, ctx_len, then the attention workspace,
-    # each on a 256-byte boundary
+    # regions: q, k, v, ctx, act, ctx_len, then the attention workspace, each
+    # on a 256-byte boundary
     up = lambda x: (x + 255) // 256 * 256
     H, qd, kvd, Hq, d, I = 4096, 4096, 1024, 32, 128, 14336
     attn = dlmk.dlmk_paged_attention_workspace_size(1, 1, Hq, d, 16, 256)
     off = 0
-    for n in (H, qd, kvd, kvd, qd, I, 1):
+    for n in (qd, kvd, kvd, qd, I, 1):
         off = up(off + 4 * n)
     assert dlmk.dlmk_decode_block_workspace_size(H, qd, kvd, Hq, d, I, 256) == off + attn
     assert dlmk.dlmk_decode_block_workspace_size(0, qd, kvd, Hq, d, I, 256) == 0
