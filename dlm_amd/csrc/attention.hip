@@ -33,6 +33,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cmath>
+#include <type_traits>
 
 #include "dlmk.h"
 #include "dlmk_internal.h"
@@ -55,6 +56,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 #define DLMK_MFMA_PD 2
 #endif
 // Prefetch depth for int8 / int4 pools, whose tiles are 2x / 4x smaller.
+// Minimum waves per SIMD for the quantized-pool kernels: half the bytes per
+// tile leave the per-tile latency chain exposed, so they trade registers for
+// occupancy.
+#ifndef DLMK_MFMA_QWAVES
+#define DLMK_MFMA_QWAVES 3
+#endif
 #ifndef DLMK_MFMA_PDQ
 #define DLMK_MFMA_PDQ 2
 #endif
@@ -223,108 +230,158 @@ struct Mfma<__bf16> {
 };
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Exact widening of small integer codes to f16 without conversions: the f16
-// with bit pattern 0x64uu is 1024 + uu for any byte uu, so biasing a code c
-// to the unsigned byte c + B and placing it under a 0x64 high byte yields
-// 1024 + B + c, and one packed f16 subtraction of 1024 + B leaves c.
-// v_perm_b32 builds two such halves from bytes lo, lo+1 of w in one op.
-template <int BIAS, int LO>
-__device__ __forceinline__ f16x2 widen_pair(uint32_t w) {
+// with bit pattern 0x64uu is 1024 + uu for any byte uu, so a code c biased to
+// the unsigned byte c + b and placed under a 0x64 high byte is the f16 value
+// B + c with B = 1024 + b.  v_perm_b32 builds two such halves from bytes lo,
+// lo + 1 of w in one op.  The bias is not subtracted per element: the kernel
+// removes B * sum(q) from each score and B * sum(p) from each output row
+// (dot products are linear in the codes), which takes one VALU op per code
+// pair off the inner loops.  B + c is exact in f16 (|B + c| < 2048) and the
+// products are exact in the f32 accumulators, so the only extra rounding is
+// f32 accumulation of the larger partial sums (about 2^-24 * B relative to
+// the q or p magnitudes).
+template <int LO>
+__device__ __forceinline__ f16x2 biased_pair(uint32_t w) {
     constexpr uint32_t sel = 0x04000400u | (uint32_t)LO | (uint32_t)(LO + 1) << 16;
-    const uint32_t h = __builtin_amdgcn_perm(0x64646464u, w, sel);
-    return __builtin_bit_cast(f16x2, h) - f16x2{(_Float16)(1024 + BIAS), (_Float16)(1024 + BIAS)};
+    return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, sel));
 }
 
-// Four biased byte codes (bytes 0..3 of w) -> f16x4.
-template <int BIAS>
-__device__ __forceinline__ f16x4 widen4(uint32_t w) {
-    const f16x2 a = widen_pair<BIAS, 0>(w), b = widen_pair<BIAS, 2>(w);
+// Four biased byte codes (bytes 0..3 of w) -> f16x4 of B + c.
+__device__ __forceinline__ f16x4 biased4(uint32_t w) {
+    const f16x2 a = biased_pair<0>(w), b = biased_pair<2>(w);
     return f16x4{a[0], a[1], b[0], b[1]};
 }
 
-// Storage codecs of the matrix-core kernel: where a lane's K chunk (8
-// consecutive dims of one token: the A operand of S^T = K.Q^T) and V piece (4
-// consecutive tokens of one dim: the B operand of O = P.V) sit in a (block,
-// kv head) tile, and how they widen to MFMA operands.
-//   q_op: a fixed permutation of the 8 dims of a Q operand chunk, matching
-//     the order k_op emits a K chunk in (the dot product does not care).
+// Storage codecs of the matrix-core kernel, one per pool format and head
+// dim D.  A codec says where a lane's K and V bytes sit in a (block, kv head)
+// tile and how they become MFMA operands:
+//   QK (S^T = K.Q^T, 16x16x32): step i takes 8 dims of token n (lane n + 16g)
+//     from K load i / SK, sub-step i % SK; q_chunk(i, g) is the 8-dim Q chunk
+//     those 8 K dims pair with, and q_op permutes a Q chunk into the order
+//     k_op emits K in (the dot product does not care which dims pair up, only
+//     that both sides agree).
+//   PV (O = P.V, 16x16x16): step k takes 4 tokens (4g .. 4g + 3) of one dim,
+//     from V load k / SV, sub-step k % SV; its output column n is dim
+//     v_dim(k, n).
+// Each lane loads 16 bytes per instruction wherever a tile holds that many
+// per lane: the int8 kernel with 8-byte K and 4-byte V loads reached 62% of
+// the read bandwidth a pure 16-byte read of the same tiles reaches 77%.
 //   Quantized codecs keep one f32 scale per token: K scales multiply the
 //     score, V scales multiply the probabilities (p * v_scale, 4 values per
-//     lane, instead of 32 widened values).  Codes widen to f16 exactly.
-template <typename E>
-struct CodecFloat {  // f16 / bf16 pools: [d/8][16][8] and [d][16] elements
+//     lane, instead of 32 widened values).  Codes widen to f16 exactly, as
+//     kBias + code (the kernel removes the bias).
+template <typename E, int D>
+struct CodecFloat {  // f16 / bf16 pools: K [d/8][16][8], V [d][16] elements
     using QT = E;
     using Op = Mfma<E>;
     using KRaw = typename Op::x8;
     using VRaw = typename Op::x4;
     static constexpr bool kScaled = false;
-    static constexpr int kTileBytesPerDim = kBlock * sizeof(E);
+    static constexpr int kMinWaves = 1;  // memory-bound at the compiler's allocation
+    static constexpr float kBias = 0.f, kBiasK = 0.f;
+    static constexpr int64_t kTileBytes = (int64_t)D * kBlock * sizeof(E);
+    static constexpr int SK = 1, KL = D / 32, SV = 1, VL = D / 16;
     static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int i, int lane) {
         return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * i + lane);
     }
-    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int g, int n) {
+    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int lane) {
+        const int g = lane >> 4, n = lane & 15;
         return stream_load(reinterpret_cast<const VRaw *>(tile) + ((16 * k + n) * kBlock + 4 * g) / 4);
     }
+    static __device__ __forceinline__ int q_chunk(int i, int g) { return 4 * i + g; }
     static __device__ __forceinline__ KRaw q_op(KRaw q) { return q; }
-    static __device__ __forceinline__ typename Op::x8 k_op(KRaw r) { return r; }
+    static __device__ __forceinline__ typename Op::x8 k_op(KRaw r, int) { return r; }
     static __device__ __forceinline__ typename Op::x4 v_op(VRaw r, int) { return r; }
+    static __device__ __forceinline__ int v_dim(int k, int n) { return 16 * k + n; }
 };
 
-struct CodecI8 {  // int8 pools: K [d/8][16][8] bytes, V [d][16] bytes
+template <int D>
+using CodecF16 = CodecFloat<_Float16, D>;
+template <int D>
+using CodecBF16 = CodecFloat<__bf16, D>;
+
+// Quantized tiles (head dim a multiple of 64), int4 codes two to a byte with
+// the even element in the low nibble:
+//   K [D/KG][16 tokens][KG dims]: one lane load = KG dims of token n = SK
+//     QK steps (8 dims each);
+//   V [D/(16 VG)][4 token quads][16][VG dims][4 tokens]: one lane load = 4
+//     tokens x VG dims = VG PV steps, lane n holding dims VG n .. VG n + VG - 1
+//     of its quarter.
+template <int D>
+struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
     using QT = _Float16;
     using Op = Mfma<_Float16>;
-    using KRaw = u32x2;
-    using VRaw = uint32_t;
+    using KRaw = u32x4;
+    using VRaw = u32x4;
     static constexpr bool kScaled = true;
-    static constexpr int kTileBytesPerDim = kBlock;
-    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int i, int lane) {
-        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * i + lane);
+    static constexpr float kBias = 1024.f + 128.f, kBiasK = kBias;
+    static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;  // codes stored as c, widened from c + 128
+    static constexpr int64_t kTileBytes = (int64_t)D * kBlock;
+    static constexpr int SK = 2, KL = D / 64, SV = 4, VL = D / 64;
+    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int p, int lane) {
+        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * p + lane);
     }
-    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int g, int n) {
-        return stream_load(reinterpret_cast<const VRaw *>(tile + (16 * k + n) * kBlock + 4 * g));
+    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int l, int lane) {
+        return stream_load(reinterpret_cast<const VRaw *>(tile) + 64 * l + lane);
     }
+    static __device__ __forceinline__ int q_chunk(int i, int g) { return 8 * (i >> 1) + 2 * g + (i & 1); }
     static __device__ __forceinline__ f16x8 q_op(f16x8 q) { return q; }
-    static __device__ __forceinline__ f16x8 k_op(KRaw r) {
-        const f16x4 a = widen4<128>(r[0] ^ 0x80808080u), b = widen4<128>(r[1] ^ 0x80808080u);
+    static __device__ __forceinline__ f16x8 k_op(KRaw r, int s) {
+        const f16x4 a = biased4(r[2 * s] ^ 0x80808080u), b = biased4(r[2 * s + 1] ^ 0x80808080u);
         return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     }
-    static __device__ __forceinline__ f16x4 v_op(VRaw r, int) { return widen4<128>(r ^ 0x80808080u); }
+    static __device__ __forceinline__ f16x4 v_op(VRaw r, int kk) { return biased4(r[kk] ^ 0x80808080u); }
+    static __device__ __forceinline__ int v_dim(int k, int n) { return 64 * (k >> 2) + 4 * n + (k & 3); }
 };
 
-struct CodecI4 {  // int4 pools: K [d/8][16][4] bytes (two elements a byte, low nibble even), V [d/2][16] bytes
+template <int D>
+struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 64: 8-byte loads, a whole tile)
+    static constexpr bool kWide = D % 128 == 0;
+    static constexpr int KG = kWide ? 32 : 16, VG = kWide ? 8 : 4;
     using QT = _Float16;
     using Op = Mfma<_Float16>;
-    using KRaw = uint32_t;
-    using VRaw = uint32_t;
+    using KRaw = typename std::conditional<kWide, u32x4, u32x2>::type;
+    using VRaw = KRaw;
     static constexpr bool kScaled = true;
-    static constexpr int kTileBytesPerDim = kBlock / 2;
-    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int i, int lane) {
-        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * i + lane);
+    // K codes are unbiased per element: with codes of at most 7 against a
+    // bias of 1032 the f32 cancellation in the scores, scaled by a large
+    // token's K scale, reaches the output tolerance.  V keeps the bias (its
+    // error is relative to p * v_scale, which the output is divided by).
+    static constexpr float kBias = 1024.f + 8.f, kBiasK = 0.f;
+    static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;  // nibbles c widened from c + 8
+    static constexpr int64_t kTileBytes = (int64_t)D * kBlock / 2;
+    static constexpr int SK = KG / 8, KL = D / (4 * KG), SV = VG, VL = D / (16 * VG);
+    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int p, int lane) {
+        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * p + lane);
     }
-    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int g, int n) {
-        return stream_load(reinterpret_cast<const VRaw *>(tile + ((16 * k + n) >> 1) * kBlock + 4 * g));
+    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int l, int lane) {
+        return stream_load(reinterpret_cast<const VRaw *>(tile) + 64 * l + lane);
     }
-    // k_op emits elements in the order 0 2 4 6 1 3 5 7 (even nibbles, then odd).
+    static __device__ __forceinline__ int q_chunk(int i, int g) { return SK * (4 * (i / SK) + g) + i % SK; }
+    // k_op emits a word's elements in the order 0 2 4 6 1 3 5 7 (even nibbles, then odd).
     static __device__ __forceinline__ f16x8 q_op(f16x8 q) {
         return f16x8{q[0], q[2], q[4], q[6], q[1], q[3], q[5], q[7]};
     }
-    static __device__ __forceinline__ f16x8 k_op(KRaw r) {
-        const uint32_t x = r ^ 0x88888888u;  // signed nibble c -> c + 8
-        const f16x4 a = widen4<8>(x & 0x0f0f0f0fu), b = widen4<8>((x >> 4) & 0x0f0f0f0fu);
-        return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    static __device__ __forceinline__ f16x8 k_op(KRaw r, int s) {
+        const uint32_t x = r[s] ^ 0x88888888u;  // signed nibble c -> c + 8
+        const f16x4 a = biased4(x & 0x0f0f0f0fu), b = biased4((x >> 4) & 0x0f0f0f0fu);
+        const f16x8 w = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        return w - (_Float16)kBias;
     }
-    // Byte t of a V row holds dims 2p (low nibble) and 2p + 1 of token t; lane
-    // dim n takes nibble n & 1 of each of its 4 tokens.
-    static __device__ __forceinline__ f16x4 v_op(VRaw r, int n) {
-        return widen4<8>(((r >> (4 * (n & 1))) & 0x0f0f0f0fu) ^ 0x08080808u);
+    // Word kk / 2 holds dims kk & ~1 (low nibbles) and kk | 1 of 4 tokens.
+    static __device__ __forceinline__ f16x4 v_op(VRaw r, int kk) {
+        return biased4(((r[kk >> 1] >> (4 * (kk & 1))) & 0x0f0f0f0fu) ^ 0x08080808u);
     }
+    static __device__ __forceinline__ int v_dim(int k, int n) { return 16 * VG * (k / VG) + VG * n + k % VG; }
 };
 
 #if DLMK_MFMA_WPE
 #define DLMK_MFMA_ATTRS __attribute__((amdgpu_waves_per_eu(DLMK_MFMA_WPE)))
 #else
-#define DLMK_MFMA_ATTRS
+#define DLMK_MFMA_ATTRS __attribute__((amdgpu_waves_per_eu(C::kMinWaves)))
 #endif
 
 template <typename C, int D, int GQA, int NQ, int NW, int NB, int PD>
@@ -342,10 +399,10 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     using PT = typename M::elem;
     using QT = typename C::QT;
     constexpr int ROWS = GQA * NQ;
-    constexpr int KI = D / 32;           // QK steps = K chunk loads per lane per block
-    constexpr int VN = D / 16;           // PV steps = V piece loads per lane per block
+    constexpr int KI = D / 32;           // QK steps per block
+    constexpr int VN = D / 16;           // PV steps per block
     constexpr int P = NW * NB * kBlock;  // tokens per work-group
-    constexpr int64_t TILE = (int64_t)D * C::kTileBytesPerDim;  // bytes per (block, kv head)
+    constexpr int64_t TILE = C::kTileBytes;  // bytes per (block, kv head)
     static_assert(ROWS <= 16 && D % 32 == 0, "unsupported geometry");
 
     __shared__ float o_lds[NW][ROWS][D];
@@ -369,7 +426,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     const int nblk_seq = (ctx + kBlock - 1) / kBlock;
     const int32_t *table = block_tables + (int64_t)seq * max_blocks;
 
-    // Q^T operand: row n of the group, dims 32i + 8g .. +7 (zeroed beyond
+    // Q^T operand: row n of the group, chunk q_chunk(i, g) (zeroed beyond
     // ROWS below).  Lanes past ROWS load row n % ROWS, so the loads carry no
     // branches (a masked load would make its first use wait for it).
     x8 qb[KI];
@@ -378,7 +435,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         const int j = r / GQA, h = kvh * GQA + r % GQA;
         const x8 *qp = reinterpret_cast<const x8 *>(q + ((int64_t)(seq * NQ + j) * num_q_heads + h) * D);
 #pragma unroll
-        for (int i = 0; i < KI; ++i) qb[i] = qp[g + 4 * i];
+        for (int i = 0; i < KI; ++i) qb[i] = qp[C::q_chunk(i, g)];
     }
     // Causal limit of this lane's row (verify query n / GQA).
     const int limit = n < ROWS ? ctx - NQ + n / GQA + 1 : ctx;
@@ -412,6 +469,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     }
 
     float m = -INFINITY, lsum = 0.f;
+    float psum = 0.f;  // quantized pools: sum of this lane's P operand (row n)
     f32x4 acc[VN];
 #pragma unroll
     for (int k = 0; k < VN; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -443,8 +501,8 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         // blocks 0..NB-1, then V tiles): load stage t + PD is issued before
         // stage t is consumed, and scheduling barriers keep the compiler from
         // sinking the loads next to their uses.
-        typename C::KRaw kb[NB][KI];
-        typename C::VRaw vb[NB][VN];
+        typename C::KRaw kb[NB][C::KL];
+        typename C::VRaw vb[NB][C::VL];
         f32x4 ksc[NB], vsc[NB];
         // A stage's scale load goes out before its code loads, fenced by a
         // scheduling barrier: loads complete in issue order, so waiting for
@@ -457,7 +515,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
                 }
                 const uint8_t *kt = k_pool + (blk[t] * num_kv_heads + kvh) * TILE;
 #pragma unroll
-                for (int i = 0; i < KI; ++i) kb[t][i] = C::load_k(kt, i, lane);
+                for (int i = 0; i < C::KL; ++i) kb[t][i] = C::load_k(kt, i, lane);
             } else if (t < 2 * NB) {
                 if constexpr (C::kScaled) {
                     vsc[t - NB] = *reinterpret_cast<const f32x4 *>(v_scales + blk[t - NB] * kBlock + 4 * g);
@@ -465,7 +523,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
                 }
                 const uint8_t *vt = v_pool + (blk[t - NB] * num_kv_heads + kvh) * TILE;
 #pragma unroll
-                for (int k = 0; k < VN; ++k) vb[t - NB][k] = C::load_v(vt, k, g, n);
+                for (int l = 0; l < C::VL; ++l) vb[t - NB][l] = C::load_v(vt, l, lane);
             }
         };
 #pragma unroll
@@ -475,6 +533,17 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         // first tile loads are out.
 #pragma unroll
         for (int i = 0; i < KI; ++i) qb[i] = n < ROWS ? C::q_op(qb[i]) : x8{};
+        // Sum of row n's Q operand (as the MFMA sees it): the score bias is
+        // kBiasK * qsum.
+        float qsum = 0.f;
+        if constexpr (C::kBiasK != 0.f) {
+#pragma unroll
+            for (int i = 0; i < KI; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qsum += (float)qb[i][e];
+            qsum += __shfl_xor(qsum, 16);
+            qsum += __shfl_xor(qsum, 32);
+        }
 
         // Scores S^T: s[b][j] = row n, token 4g + j of block b.
         float s[NB][4];
@@ -482,10 +551,18 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         for (int b = 0; b < NB; ++b) {
             issue(b + PD);
             __builtin_amdgcn_sched_barrier(0);
-            f32x4 c = {0.f, 0.f, 0.f, 0.f};
+            // Two accumulators (even / odd steps) halve the dependent MFMA chain.
+            f32x4 c = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int i = 0; i < KI; ++i) c = M::qk(C::k_op(kb[b][i]), qb[i], c);
-            if constexpr (C::kScaled) c *= ksc[b];
+            for (int i = 0; i < KI; i += 2) {
+                c = M::qk(C::k_op(kb[b][i / C::SK], i % C::SK), qb[i], c);
+                c1 = M::qk(C::k_op(kb[b][(i + 1) / C::SK], (i + 1) % C::SK), qb[i + 1], c1);
+            }
+            c += c1;
+            if constexpr (C::kScaled) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) c[j] = fmaf(-C::kBiasK, qsum, c[j]) * ksc[b][j];
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
                 const int pos = lbs[b] * kBlock + 4 * g + j;
@@ -515,7 +592,9 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
             x4 pa;
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                const float p = m == -INFINITY ? 0.f : exp2f(s[b][j] - m);
+                // v_exp_f32 directly: s - m <= 0 (or -inf, giving 0), and
+                // results below 2^-126 (flushed) do not matter next to the row max's 1.
+                const float p = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[b][j] - m);
                 if constexpr (C::kScaled) {
                     // p is 0 there already; the select keeps a NaN scale out.
                     pa[j] = (PT)(4 * g + j < valid ? p * vsc[b][j] : 0.f);
@@ -526,9 +605,16 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
                     lsum += (float)ph;
                 }
             }
+            if constexpr (C::kScaled) {
+                // Exact sum of the operand the MFMA sees, subnormals included
+                // (v_dot2_f32_f16 is not: the bias turns any difference into
+                // kBias times that much output error).
+#pragma unroll
+                for (int j = 0; j < 4; ++j) psum += (float)pa[j];
+            }
             typename M::x4 vo[VN];
 #pragma unroll
-            for (int k = 0; k < VN; ++k) vo[k] = C::v_op(vb[b][k], n);
+            for (int k = 0; k < VN; ++k) vo[k] = C::v_op(vb[b][k / C::SV], k % C::SV);
             if constexpr (!C::kScaled) {
                 // Float V can hold NaN past the context, and 0 * NaN is NaN:
                 // zero it.  A wave-uniform branch, taken only by partial blocks.
@@ -547,13 +633,25 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     }
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
+    if constexpr (C::kScaled) {
+        // Output bias of row 4g + j: kBias * (row's P sum), held by lane 4g + j.
+        psum += __shfl_xor(psum, 16);
+        psum += __shfl_xor(psum, 32);
+        float ob[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ob[j] = C::kBias * __shfl(psum, 4 * g + j);
+#pragma unroll
+        for (int k = 0; k < VN; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[k][j] -= ob[j];
+    }
 
-    // acc[k][j] = O[row 4g + j][dim 16k + n].
+    // acc[k][j] = O[row 4g + j][dim v_dim(k, n)].
 #pragma unroll
     for (int k = 0; k < VN; ++k)
 #pragma unroll
         for (int j = 0; j < 4; ++j)
-            if (4 * g + j < ROWS) o_lds[wave][4 * g + j][16 * k + n] = acc[k][j];
+            if (4 * g + j < ROWS) o_lds[wave][4 * g + j][C::v_dim(k, n)] = acc[k][j];
     if (g == 0 && n < ROWS) {
         ml_lds[wave][n][0] = m;
         ml_lds[wave][n][1] = lsum;
@@ -905,8 +1003,9 @@ int unsupported_rows(int gqa, int nq) {
                       "paged attention: no kernel for GQA group %d x %d queries", gqa, nq);
 }
 
-template <typename C, int D>
+template <template <int> class CD, int D>
 int dispatch_mfma(const Args &a, int gqa) {
+    using C = CD<D>;
     switch (gqa * 16 + a.NQ) {
         case 1 * 16 + 1: return launch_mfma<C, D, 1, 1>(a);
         case 1 * 16 + 2: return launch_mfma<C, D, 1, 2>(a);
@@ -1047,16 +1146,16 @@ int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype
             }
         case DLMK_F16:
             switch (head_dim) {
-                case 64: return dispatch_mfma<CodecFloat<_Float16>, 64>(a, gqa);
-                case 128: return dispatch_mfma<CodecFloat<_Float16>, 128>(a, gqa);
-                case 256: return dispatch_mfma<CodecFloat<_Float16>, 256>(a, gqa);
+                case 64: return dispatch_mfma<CodecF16, 64>(a, gqa);
+                case 128: return dispatch_mfma<CodecF16, 128>(a, gqa);
+                case 256: return dispatch_mfma<CodecF16, 256>(a, gqa);
                 default: return bad_dim(head_dim, "64, 128, 256");
             }
         case DLMK_BF16:
             switch (head_dim) {
-                case 64: return dispatch_mfma<CodecFloat<__bf16>, 64>(a, gqa);
-                case 128: return dispatch_mfma<CodecFloat<__bf16>, 128>(a, gqa);
-                case 256: return dispatch_mfma<CodecFloat<__bf16>, 256>(a, gqa);
+                case 64: return dispatch_mfma<CodecBF16, 64>(a, gqa);
+                case 128: return dispatch_mfma<CodecBF16, 128>(a, gqa);
+                case 256: return dispatch_mfma<CodecBF16, 256>(a, gqa);
                 default: return bad_dim(head_dim, "64, 128, 256");
             }
         case DLMK_I8:

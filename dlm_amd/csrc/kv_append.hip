@@ -80,12 +80,14 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 //
 // One wavefront per token.  Lane l owns the 8-dim chunks l, l + 64, ... of
 // the token (NC of them, kept in registers): one 16-byte source load per chunk
-// (two for f32), a wave max-reduction, then one store per chunk for K
-// (int8 K [d/8][16][8]: 8 bytes; int4 K [d/8][16][4]: 4 bytes) and 8 / 4 byte
-// stores for V (int8 V [d][16]; int4 V [d/2][16], a byte holding dims 2p and
-// 2p + 1 of one token, low nibble 2p, so a byte never mixes tokens and
-// appends never share one).
-// ---------------------------------------------------------------------------
+// (two for f32), a wave max-reduction, then the stores into the tiles the
+// attention kernel reads 16 bytes a lane at a time (head_dim a multiple of
+// 64; KG, VG as below):
+//   K [d/KG][16 tokens][KG dims], KG = 16 (int8) or 32 / 16 (int4, d % 128
+//     == 0 or not): a chunk is one 8-byte (int8) or 4-byte (int4) store;
+//   V [d/(16 VG)][4 token quads][16][VG dims][4 tokens], VG = 4 (int8) or
+//     8 / 4 (int4): one byte per dim (int8) or per dim pair (int4, low nibble
+//     the even dim, so a byte never mixes tokens and appends never share one).
 template <typename S>
 __device__ __forceinline__ void load8(const S *p, float (&x)[8]) {
     if constexpr (sizeof(S) == 4) {
@@ -127,6 +129,11 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
     const int d = head_dim, kv_dim = num_kv_heads * head_dim, nchunks = kv_dim / 8;
     const float qmax = QBITS == 8 ? 127.f : 7.f;
     const int64_t tile_bytes = (int64_t)d * BS * QBITS / 8;
+    // Tile geometry (see above): KG dims per K chunk, VG dims per V lane
+    // group, VLANE bytes per V lane group.
+    const int KG = QBITS == 8 ? 16 : (d % 128 == 0 ? 32 : 16);
+    const int VG = QBITS == 8 ? 4 : (d % 128 == 0 ? 8 : 4);
+    const int VLANE = VG * QBITS / 2;
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
         const S *src = (which ? v_src : k_src) + tok * kv_dim;
@@ -159,15 +166,20 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
             int q[8];
 #pragma unroll
             for (int k = 0; k < 8; ++k) q[k] = quant_code(x[i][k], ok, scale, qmax);
+            // V: dim jj of this token sits at lane group (jj / VG) % 16 of
+            // quarter jj / (16 VG), word (jj % VG) / (dims per byte), byte t % 4.
+            const int vq = j / (16 * VG), vn = (j % (16 * VG)) / VG, vk = j % VG;
+            uint8_t *vbase = tile + ((int64_t)(vq * 4 + t / 4) * 16 + vn) * VLANE + t % 4;
             if constexpr (QBITS == 8) {
                 if (which == 0) {
                     u32x2 w;
                     w[0] = (q[0] & 0xff) | (q[1] & 0xff) << 8 | (q[2] & 0xff) << 16 | (uint32_t)(q[3] & 0xff) << 24;
                     w[1] = (q[4] & 0xff) | (q[5] & 0xff) << 8 | (q[6] & 0xff) << 16 | (uint32_t)(q[7] & 0xff) << 24;
-                    *reinterpret_cast<u32x2 *>(tile + ((j / 8) * BS + t) * 8) = w;
+                    *reinterpret_cast<u32x2 *>(tile + ((j / KG) * BS + t) * KG + j % KG) = w;
                 } else {
+                    // 8 dims = two lane groups of VG = 4 (vk == 0).
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) tile[(j + k) * BS + t] = (uint8_t)q[k];
+                    for (int k = 0; k < 8; ++k) vbase[(k / 4) * VLANE + (k % 4) * 4] = (uint8_t)q[k];
                 }
             } else {
                 uint8_t by[4];
@@ -176,10 +188,15 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
                     by[m] = (uint8_t)((q[2 * m] & 0x0f) | (q[2 * m + 1] & 0x0f) << 4);
                 if (which == 0) {
                     uint32_t w = by[0] | by[1] << 8 | by[2] << 16 | (uint32_t)by[3] << 24;
-                    *reinterpret_cast<uint32_t *>(tile + ((j / 8) * BS + t) * 4) = w;
+                    *reinterpret_cast<uint32_t *>(tile + ((j / KG) * BS + t) * (KG / 2) + (j % KG) / 2) = w;
                 } else {
+                    // Dim pair m of the chunk: VG = 8 keeps the chunk in one
+                    // lane group (words vk/2 .. +3); VG = 4 spans two (vk == 0).
 #pragma unroll
-                    for (int m = 0; m < 4; ++m) tile[(j / 2 + m) * BS + t] = by[m];
+                    for (int m = 0; m < 4; ++m) {
+                        const int jj = vk + 2 * m;
+                        vbase[(jj / VG) * VLANE + ((jj % VG) / 2) * 4] = by[m];
+                    }
                 }
             }
         }
@@ -239,9 +256,9 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_kv_append_quant: null pointer");
     if (quant != DLMK_I8 && quant != DLMK_I4)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_kv_append_quant: quant %d is not int8/int4", quant);
-    if (head_dim % 8 != 0 || block_size != 16)
+    if (head_dim % 64 != 0 || block_size != 16)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED,
-                          "dlmk_kv_append_quant: head_dim %d (multiple of 8) / block_size %d (16)",
+                          "dlmk_kv_append_quant: head_dim %d (multiple of 64) / block_size %d (16)",
                           head_dim, block_size);
     const int64_t kv_dim = (int64_t)num_kv_heads * head_dim;
     const int64_t chunks_per_lane = dlmk::ceil_div(kv_dim / 8, 64);

@@ -269,18 +269,19 @@ class QuantKv:
 
 def alloc_quant_pools(num_blocks: int, num_kv_heads: int, head_dim: int, quant: str,
                       device="cuda", block_size: int = BLOCK_SIZE) -> QuantKv:
-    """Allocate one layer's int8 / int4 pools in the library's layout:
-    int8 K [nb, Hkv, d/8, 16, 8], V [nb, Hkv, d, 16]; int4 K [nb, Hkv, d/8, 16, 4],
-    V [nb, Hkv, d/2, 16]; scales [nb, 16] float32 (zero)."""
+    """Allocate one layer's int8 / int4 pools in the library's layout (head_dim
+    a multiple of 64; int4 codes two to a byte):
+    K [nb, Hkv, d/KG, 16, KG], V [nb, Hkv, d/(16 VG), 4, 16, 4 VG] with KG, VG =
+    16, 4 for int8 and 32, 8 (d % 128 == 0) or 16, 4 for int4; scales [nb, 16]
+    float32 (zero)."""
     if quant not in _QUANT:
         raise ValueError(f"quant must be int8 or int4 (got {quant!r})")
-    if head_dim % 8 != 0:
-        raise ValueError("head_dim must be a multiple of 8")
+    if head_dim % 64 != 0:
+        raise ValueError("head_dim must be a multiple of 64")
     nb, H, d, bs = num_blocks, num_kv_heads, head_dim, block_size
-    if quant == "int8":
-        ks, vs = (nb, H, d // 8, bs, 8), (nb, H, d, bs)
-    else:
-        ks, vs = (nb, H, d // 8, bs, 4), (nb, H, d // 2, bs)
+    kg, vg = (16, 4) if quant == "int8" or d % 128 else (32, 8)
+    per = 1 if quant == "int8" else 2
+    ks, vs = (nb, H, d // kg, bs, kg // per), (nb, H, d // (16 * vg), 4, 16, 4 * vg // per)
     return QuantKv(torch.zeros(ks, dtype=torch.uint8, device=device),
                    torch.zeros(vs, dtype=torch.uint8, device=device),
                    torch.zeros((nb, bs), dtype=torch.float32, device=device),

@@ -237,17 +237,23 @@ int dlmk_paged_decode_step(void *stream, void *out, int out_dtype, const void *q
  * src/forward/cpu.rs:622-711).  Each token carries one f32 scale per pool over
  * its whole kv_dim (num_kv_heads * head_dim values): scale = max|x| / qmax
  * (qmax 127 / 7), code = round-half-away(x / scale) clamped to +-qmax, and an
- * all-zero token has scale 0 and zero codes.  Layouts per layer (block_size 16):
- *   int8: K [num_blocks][Hkv][d/8][16][8] bytes, V [num_blocks][Hkv][d][16] bytes
- *   int4: K [num_blocks][Hkv][d/8][16][4] bytes (two elements a byte, low
- *         nibble the even one), V [num_blocks][Hkv][d/2][16] bytes (dims 2p and
- *         2p+1 of one token in one byte, low nibble 2p)
+ * all-zero token has scale 0 and zero codes.  head_dim is a multiple of 64.
+ * Layouts per layer (block_size 16), int4 codes two to a byte (low nibble
+ * the even element), each (block, kv head) tile:
+ *   K [d/KG][16 tokens][KG dims]: KG = 16 (int8); int4 KG = 32 if
+ *     d % 128 == 0, else 16.
+ *   V [d/(16 VG)][4 token quads][16][VG dims][4 tokens]: VG = 4 (int8);
+ *     int4 VG = 8 if d % 128 == 0, else 4 (an int4 byte holds one token's
+ *     dims 2p and 2p+1).  Dim j of token t sits at quarter j / (16 VG), quad
+ *     t / 4, group (j / VG) % 16, element j % VG, token t % 4.
  *   scales: k_scales / v_scales f32 [num_blocks][16] (slot order).
+ * Each lane of the attention kernel loads 16 bytes of a tile at a time (8 at
+ * int4 d = 64, where a whole tile is 512 bytes).
  * Append: replaces KvLayerCache::append's quantizing branch (cpu.rs:765-795,
  * quantize_i8 / quantize_i4 at :672-711).  k_src / v_src are
  * [n_tok][num_kv_heads][head_dim] in src_dtype (f32, f16, bf16); token i goes
  * to slot_mapping[i]; negative or out-of-pool slots are skipped.  quant is
- * DLMK_I8 or DLMK_I4; head_dim a multiple of 8. */
+ * DLMK_I8 or DLMK_I4. */
 int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, float *k_scales,
                          float *v_scales, const void *k_src, const void *v_src, int src_dtype,
                          const int64_t *slot_mapping, int64_t n_tok, int num_kv_heads,

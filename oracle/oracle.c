@@ -618,14 +618,17 @@ void orc_quantize_tokens(const float *src, int64_t n_tok, int64_t kv_dim, int qu
     }
 }
 
-/* Paged quantized pools (layout of this build, no reference counterpart):
- *   K codes: int8 [nb][Hkv][d/8][16][8] bytes; int4 [nb][Hkv][d/8][16][4]
- *            (8 consecutive dims per chunk, element e in byte e/2, low nibble
- *            for even e)
- *   V codes: int8 [nb][Hkv][d][16] bytes;     int4 [nb][Hkv][d/2][16]
- *            (byte (p, t) = dims 2p and 2p+1 of token t, low nibble for the
- *            even dim: a byte never mixes tokens, so appends never share one)
- *   scales:  K and V f32 [nb][16], one per token (shared by all heads). */
+/* Paged quantized pools (layout of this build, no reference counterpart).
+ * head_dim d is a multiple of 64.  Elements are 8-bit codes (int8) or 4-bit
+ * codes two to a byte (int4, low nibble the even element).
+ *   K tile of one (block, kv head): [d/KG][16 tokens][KG dims], KG = 16
+ *     (int8) or, for int4, 32 when d % 128 == 0 else 16 -- one token's KG
+ *     consecutive dims fill 16 bytes (8 for int4 at d = 64).
+ *   V tile: [d/(16 VG)][4 token quads][16 dim groups][VG dims][4 tokens],
+ *     VG = 4 (int8) or, for int4, 8 when d % 128 == 0 else 4; an int4 byte
+ *     holds one token's dims 2p, 2p + 1 (low nibble 2p), so a byte never
+ *     mixes tokens and appends never share one.
+ *   scales: K and V f32 [nb][16], one per token (shared by all heads). */
 static void put_nibble(uint8_t *b, int hi, int code) {
     uint8_t nib = (uint8_t)code & 0x0f;
     *b = hi ? (uint8_t)((*b & 0x0f) | (nib << 4)) : (uint8_t)((*b & 0xf0) | nib);
@@ -635,14 +638,24 @@ static int get_nibble(const uint8_t *b, int hi) {
     return nib >= 8 ? nib - 16 : nib;
 }
 
+int orc_quant_k_group(int d, int quant) { return quant == ORC_I8 ? 16 : (d % 128 == 0 ? 32 : 16); }
+int orc_quant_v_group(int d, int quant) { return quant == ORC_I8 ? 4 : (d % 128 == 0 ? 8 : 4); }
+
+/* Byte offset of element (token t, dim j) of kv head h in block blk; for int4
+ * the element is nibble j % 2 of that byte. */
 static int64_t qk_off(int64_t blk, int h, int t, int j, int Hkv, int d, int quant) {
-    int64_t tile = (blk * Hkv + h) * (int64_t)d * 16;  /* elements */
-    int64_t el = tile + ((int64_t)(j / 8) * 16 + t) * 8 + (j % 8);
-    return quant == ORC_I8 ? el : el / 2; /* byte offset (int4: nibble el % 2) */
+    int64_t tile = (blk * Hkv + h) * (int64_t)d * 16 * (quant == ORC_I8 ? 2 : 1) / 2;
+    int kg = orc_quant_k_group(d, quant);
+    int64_t el = ((int64_t)(j / kg) * 16 + t) * kg + (j % kg);
+    return tile + (quant == ORC_I8 ? el : el / 2);
 }
 static int64_t qv_off(int64_t blk, int h, int t, int j, int Hkv, int d, int quant) {
-    if (quant == ORC_I8) return (blk * Hkv + h) * (int64_t)d * 16 + (int64_t)j * 16 + t;
-    return ((blk * Hkv + h) * (int64_t)(d / 2) + j / 2) * 16 + t; /* nibble j % 2 */
+    int64_t tile = (blk * Hkv + h) * (int64_t)d * 16 * (quant == ORC_I8 ? 2 : 1) / 2;
+    int vg = orc_quant_v_group(d, quant), per = 16 * vg;
+    int q = j / per, r = j % per, n = r / vg, kk = r % vg;
+    int lane_bytes = quant == ORC_I8 ? 4 * vg : 2 * vg;
+    int word = quant == ORC_I8 ? kk : kk / 2;
+    return tile + ((int64_t)(q * 4 + t / 4) * 16 + n) * lane_bytes + word * 4 + t % 4;
 }
 
 /* Quantize n_tok tokens (src [n][Hkv][d] f32) and scatter codes + scales. */
@@ -671,7 +684,7 @@ void orc_paged_append_quant(void *k_pool, void *v_pool, float *k_scales, float *
                     ((int8_t *)k_pool)[ko] = (int8_t)kq;
                     ((int8_t *)v_pool)[vo] = (int8_t)vq;
                 } else {
-                    put_nibble((uint8_t *)k_pool + ko, (j % 8) % 2, kq);
+                    put_nibble((uint8_t *)k_pool + ko, j % 2, kq);
                     put_nibble((uint8_t *)v_pool + vo, j % 2, vq);
                 }
             }
@@ -705,7 +718,7 @@ void orc_paged_gather_quant(const void *k_pool, const void *v_pool, const float 
                 } else {
                     uint8_t *kb = (uint8_t *)kcodes + p * rb + e / 2;
                     uint8_t *vb = (uint8_t *)vcodes + p * rb + e / 2;
-                    put_nibble(kb, (int)(e % 2), get_nibble((const uint8_t *)k_pool + ko, (j % 8) % 2));
+                    put_nibble(kb, (int)(e % 2), get_nibble((const uint8_t *)k_pool + ko, j % 2));
                     put_nibble(vb, (int)(e % 2), get_nibble((const uint8_t *)v_pool + vo, j % 2));
                 }
             }

@@ -386,14 +386,28 @@ def attention_quant(q, kcodes, kscales, vcodes, vscales, num_heads, num_kv_heads
     return ctx
 
 
-def quant_pool_shapes(num_blocks, Hkv, d, quant, bs=16):
+def quant_groups(d, quant):
+    """(KG, VG): dims per K chunk and per V lane group of the paged quantized
+    tiles (orc_quant_k_group / orc_quant_v_group)."""
+    if d % 64:
+        raise ValueError("quantized pools need head_dim % 64 == 0")
     if quant == I8:
-        return (num_blocks, Hkv, d // 8, bs, 8), (num_blocks, Hkv, d, bs)
-    return (num_blocks, Hkv, d // 8, bs, 4), (num_blocks, Hkv, d // 2, bs)
+        return 16, 4
+    return (32, 8) if d % 128 == 0 else (16, 4)
+
+
+def quant_pool_shapes(num_blocks, Hkv, d, quant, bs=16):
+    """K [nb][Hkv][d/KG][16][KG codes], V [nb][Hkv][d/(16 VG)][4][16][VG * 4 codes]
+    (int4 codes two to a byte)."""
+    kg, vg = quant_groups(d, quant)
+    per = 2 if quant == I4 else 1
+    return ((num_blocks, Hkv, d // kg, bs, kg // per),
+            (num_blocks, Hkv, d // (16 * vg), 4, 16, 4 * vg // per))
 
 
 def paged_append_quant(k_pool, v_pool, k_scales, v_scales, k_src, v_src, slots, Hkv, d, quant,
                        bs=16):
+    quant_groups(d, quant)
     slots = np.ascontiguousarray(slots, np.int64)
     k_src = np.ascontiguousarray(k_src, np.float32)
     v_src = np.ascontiguousarray(v_src, np.float32)
@@ -403,6 +417,7 @@ def paged_append_quant(k_pool, v_pool, k_scales, v_scales, k_src, v_src, slots, 
 
 
 def paged_gather_quant(k_pool, v_pool, k_scales, v_scales, table, ctx, Hkv, d, quant, bs=16):
+    quant_groups(d, quant)
     rb = quant_row_bytes(Hkv * d, quant)
     dt = np.int8 if quant == I8 else np.uint8
     kc, vc = np.zeros((ctx, rb), dt), np.zeros((ctx, rb), dt)

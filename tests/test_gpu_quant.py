@@ -98,7 +98,7 @@ def assert_pools_equal(kv, kp, vp, ksc, vsc, what):
     ("f32", 8, 64, 200),    # config-1 geometry
     ("f16", 8, 128, 700),   # config-2 geometry, prefill chunk + decode tokens
     ("bf16", 2, 256, 90),
-    ("f16", 1, 8, 33),      # smallest head dim
+    ("f16", 1, 64, 33),     # one head, smallest head dim
 ])
 def test_kv_append_quant_bit_exact(oracle, torch_mod, ops, cuda, qname, src, Hkv, d, ntok):
     torch = torch_mod
@@ -140,6 +140,16 @@ def test_kv_append_quant_rejects_bad_shapes(torch_mod, ops, cuda):
     with pytest.raises(ValueError):
         ops.kv_append_quant(kv, k, k, torch.zeros(3, dtype=torch.int64, device=cuda),
                             num_kv_heads=2, head_dim=128)
+    with pytest.raises(ValueError):  # the 16-byte tiles need head_dim % 64 == 0
+        ops.alloc_quant_pools(4, 2, 32, "int4", cuda)
+    from dlm_amd._lib import DlmkError, check, lib
+    k32 = torch.zeros((3, 2, 32), dtype=torch.float16, device=cuda)
+    with pytest.raises(DlmkError):
+        check(lib().dlmk_kv_append_quant(None, kv.k.data_ptr(), kv.v.data_ptr(),
+                                         kv.k_scales.data_ptr(), kv.v_scales.data_ptr(),
+                                         k32.data_ptr(), k32.data_ptr(), 1,
+                                         torch.zeros(3, dtype=torch.int64, device=cuda).data_ptr(),
+                                         3, 2, 32, 16, 4, 3))
 
 
 # --------------------------------------------------------------- attention

@@ -334,12 +334,13 @@ def test_quant_attention_matches_dequantized_f64(oracle, quant):
     assert np.abs(got - ref).max() < 1e-5
 
 
+@pytest.mark.parametrize("d", [64, 128])
 @pytest.mark.parametrize("quant", [3, 4])
-def test_paged_quant_round_trip_and_attention(oracle, quant):
+def test_paged_quant_round_trip_and_attention(oracle, quant, d):
     """Paged quantized append -> gather reproduces the contiguous codes and scales
     byte for byte; paged attention equals contiguous quantized attention bitwise."""
-    rng = np.random.default_rng(60 + quant)
-    Hq, Hkv, d, nb, ntok = 8, 2, 32, 12, 70
+    rng = np.random.default_rng(60 + quant + d)
+    Hq, Hkv, nb, ntok = 8, 2, 12, 70
     ks_shape, vs_shape = oracle.quant_pool_shapes(nb, Hkv, d, quant)
     dt = np.int8 if quant == 3 else np.uint8
     kp = rng.integers(-100, 100, ks_shape).astype(dt)
@@ -366,3 +367,55 @@ def test_paged_quant_round_trip_and_attention(oracle, quant):
         n = ntok - 2 + j + 1
         ref = oracle.attention_quant(q[0, j], kc[:n], ks[:n], vc[:n], vs[:n], Hq, Hkv, d, quant, 0.25)
         assert np.array_equal(out[0, j].reshape(-1), ref)
+
+
+def _unpack_codes(c, quant):
+    """Contiguous codes [n, row_bytes] -> signed values [n, kv_dim]."""
+    if quant == 3:
+        return c.astype(np.int16)
+    u = c.view(np.uint8)
+    lo, hi = (u & 15).astype(np.int16), (u >> 4).astype(np.int16)
+    x = np.stack([lo, hi], -1).reshape(len(c), -1)
+    return np.where(x >= 8, x - 16, x)
+
+
+def _pack_tile_codes(vals, quant):
+    """Signed values whose last axis runs over consecutive elements -> bytes."""
+    if quant == 3:
+        return vals.astype(np.int8).view(np.uint8)
+    u = (vals & 15).astype(np.uint8)
+    return u[..., 0::2] | (u[..., 1::2] << 4)
+
+
+@pytest.mark.parametrize("d", [64, 128, 256])
+@pytest.mark.parametrize("quant", [3, 4])
+def test_paged_quant_layout_by_axes(oracle, quant, d):
+    """The paged quantized layout, restated as numpy axis permutations of the
+    [token][head][dim] codes and compared with the oracle's append byte for
+    byte over one full block per head:
+      K [d/KG][16 tokens][KG dims];  V [d/(16 VG)][4 quads][16][VG dims][4 tokens],
+    with KG, VG = 16, 4 (int8) and 32, 8 or 16, 4 (int4, d % 128 == 0 or not)."""
+    Hkv, bs = 2, 16
+    kg, vg = (16, 4) if quant == 3 else ((32, 8) if d % 128 == 0 else (16, 4))
+    assert oracle.quant_groups(d, quant) == (kg, vg)
+    rng = np.random.default_rng(d + quant)
+    k = rng.standard_normal((bs, Hkv * d)).astype(np.float32)
+    v = rng.standard_normal((bs, Hkv * d)).astype(np.float32)
+    ks_shape, vs_shape = oracle.quant_pool_shapes(2, Hkv, d, quant)
+    kp, vp = np.zeros(ks_shape, np.uint8), np.zeros(vs_shape, np.uint8)
+    ksc, vsc = np.zeros(2 * bs, np.float32), np.zeros(2 * bs, np.float32)
+    oracle.paged_append_quant(kp, vp, ksc, vsc, k, v, np.arange(bs, 2 * bs), Hkv, d, quant)
+    kc, _ = oracle.quantize_tokens(k, quant)
+    vc, _ = oracle.quantize_tokens(v, quant)
+    kx = _unpack_codes(kc, quant).reshape(bs, Hkv, d)
+    vx = _unpack_codes(vc, quant).reshape(bs, Hkv, d)
+    # K: [h][t][d] -> [h][d/KG][t][KG]
+    kt = kx.transpose(1, 0, 2).reshape(Hkv, bs, d // kg, kg).transpose(0, 2, 1, 3)
+    # V: dim j = (qq * 16 + n) * VG + kk, token t = 4 * quad + tt
+    vt = vx.transpose(1, 0, 2).reshape(Hkv, 4, 4, d // (16 * vg), 16, vg)  # h, quad, tt, qq, n, kk
+    vt = vt.transpose(0, 3, 1, 4, 5, 2)                                      # h, qq, quad, n, kk, tt
+    if quant == 4:  # an int4 byte holds one token's dims kk, kk + 1
+        vt = vt.reshape(Hkv, d // (16 * vg), 4, 16, vg // 2, 2, 4).transpose(0, 1, 2, 3, 4, 6, 5)
+    assert np.array_equal(kp[1], _pack_tile_codes(kt, quant).reshape(kp[1].shape))
+    assert np.array_equal(vp[1], _pack_tile_codes(vt, quant).reshape(vp[1].shape))
+    assert not kp[0].any() and not vp[0].any()
