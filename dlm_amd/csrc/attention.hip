@@ -413,7 +413,12 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     // with the (sequence, head) pair fastest every XCD gets the same mix of
     // full and ragged partitions (partition-fastest would pin each XCD to one
     // partition index, and late partitions exist only for long contexts).
-    const int part = blockIdx.y, kvh = blockIdx.x % num_kv_heads, seq = blockIdx.x / num_kv_heads;
+    // Partitions are dealt last index first: the high indices (long contexts
+    // only, mostly full) start early and the grid ends on partition 0, where
+    // the short sequences' small work-groups fill the drain (+1 point of HBM
+    // peak over first-index-first at the 8B shape).
+    const int part = gridDim.y - 1 - blockIdx.y, kvh = blockIdx.x % num_kv_heads,
+              seq = blockIdx.x / num_kv_heads;
     // A length beyond the table width is clamped: no read past a table row and
     // no partition index past max_parts.
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
@@ -696,7 +701,12 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
     // with the (sequence, head) pair fastest every XCD gets the same mix of
     // full and ragged partitions (partition-fastest would pin each XCD to one
     // partition index, and late partitions exist only for long contexts).
-    const int part = blockIdx.y, kvh = blockIdx.x % num_kv_heads, seq = blockIdx.x / num_kv_heads;
+    // Partitions are dealt last index first: the high indices (long contexts
+    // only, mostly full) start early and the grid ends on partition 0, where
+    // the short sequences' small work-groups fill the drain (+1 point of HBM
+    // peak over first-index-first at the 8B shape).
+    const int part = gridDim.y - 1 - blockIdx.y, kvh = blockIdx.x % num_kv_heads,
+              seq = blockIdx.x / num_kv_heads;
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
     const int nparts = parts_of(ctx, P);
     if (part >= nparts) return;
