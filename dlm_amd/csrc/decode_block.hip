@@ -11,13 +11,13 @@
 // registers, as the reference's load_w<> does.
 //
 // Kernels (all HBM-bound on the weights at decode batch 1):
-//   gemv_kernel          x staged once per work-group in LDS as f32 (both
-//                        rmsnorms are folded into that staging); a grid of
-//                        resident work-groups; one wave per output row,
+//   gemv_kernel          x staged once per work-group in LDS as f32 planes
+//                        (both rmsnorms are folded into that staging); a grid
+//                        of resident work-groups; RW output rows per wave,
 //                        16-byte weight loads, 16 in flight per lane (8 per
-//                        matrix for SwiGLU), wave reduction; epilogue = bias
-//                        store, residual add, or (two matrices) SwiGLU; q, k
-//                        and v as one launch.
+//                        matrix for SwiGLU) plus the next step's prefetched,
+//                        wave reduction; epilogue = bias store, residual add,
+//                        or (two matrices) SwiGLU; q, k and v as one launch.
 //   rope_append_kernel   RoPE on q and k (NeoX split-half, host-computed
 //                        inv_freq), then the new token's K and V straight into
 //                        the pools at the slot the block table gives; also
@@ -35,7 +35,10 @@
 namespace {
 
 constexpr int kBlock = 16;  // tokens per KV block
-constexpr int kGemvWaves = 4;
+#ifndef DLMK_GEMV_WAVES
+#define DLMK_GEMV_WAVES 4
+#endif
+constexpr int kGemvWaves = DLMK_GEMV_WAVES;
 constexpr int kGemvUnroll = 8;  // 16-byte weight loads in flight per lane
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -191,22 +194,93 @@ struct GemvArgs {
 // and x staged once in LDS as f32 -- normalised on the way when norm_w is set
 // (rmsnorm, src/forward/cpu.rs:934-943: every work-group sums the squares in
 // the same order, so all see the same factor).  Wave w of work-group b takes
-// launch rows b * kGemvWaves + w + k * gridDim.x * kGemvWaves, so a grid of
-// resident work-groups amortises the staging over several rows.  One row per
-// wave at a time: 16-byte weight loads, U in flight per lane, a wave
-// reduction.  Epilogues: kStoreBias out[o] = dot (+ bias[o]); kAddInto
-// out[o] += dot (the residual); kSwiGLU out[o] = silu(dot(W)) * dot(W2).
+// launch rows (b * kGemvWaves + w) * RW + k * gridDim.x * kGemvWaves * RW,
+// RW rows at a time, so a grid of resident work-groups amortises the staging
+// over several rows and each x read over RW rows: 16-byte weight loads, U in
+// flight per lane per row, a wave reduction per row.  Epilogues: kStoreBias
+// out[o] = dot (+ bias[o]); kAddInto out[o] += dot (the residual); kSwiGLU
+// out[o] = silu(dot(W)) * dot(W2).
+//
+// Measured on the 8B layer (bf16): the x reads from LDS, not the weight
+// stream, bounded these kernels -- down_proj took 34.9 us with the dot
+// products and 20.9 us with them replaced by a register-only reduction, against
+// 18.1 us for a pure read of its weights with the same grid.  Conflict-free
+// planes of x and one x read per RW rows took it to 23.3 us.
+template <int RW>
+struct RowGroup {  // RW launch rows resolved to their segments
+    GemvSeg g[RW];
+    int o[RW];
+    QOffsets qo[RW];
+};
+
 template <int DT, int EPI, int RW, int U>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     using C = WChunk<DT>;
     constexpr int E = C::E;
+    constexpr bool kTwo = EPI == kSwiGLU;
     extern __shared__ float xs[];
     __shared__ float red[kGemvWaves];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int in_dim = a.in_dim;
+    const int chunks = in_dim / E;
+    const int64_t row_bytes = (int64_t)in_dim * 16 / E;
+    const int rstride = gridDim.x * kGemvWaves * RW;
+
+    // A wave's work is a sequence of steps (RW rows, chunk block c0 of U * 64
+    // chunks): rows r0, r0 + rstride, ..., each over c0 = 0, 64U, ... .  The
+    // loads of step s + 1 are issued before step s is computed (two register
+    // buffers, A and B), and the first step's loads go out before x is
+    // staged, so the weight stream never waits on the x round trip or on a
+    // step's arithmetic.
+    auto resolve = [&](int r0, RowGroup<RW> &R) {
+#pragma unroll
+        for (int j = 0; j < RW; ++j) {
+            // Segment of launch row r0 + j (explicit selects: a dynamically
+            // indexed kernel-argument array would be copied to scratch).  Rows
+            // past the end repeat the last row, and are not stored.
+            int rr = min(r0 + j, a.total_rows - 1);
+            R.g[j] = a.seg[0];
+            if (a.nseg > 1 && rr >= a.seg[0].rows) {
+                rr -= a.seg[0].rows;
+                R.g[j] = a.seg[1];
+                if (a.nseg > 2 && rr >= a.seg[1].rows) {
+                    rr -= a.seg[1].rows;
+                    R.g[j] = a.seg[2];
+                }
+            }
+            R.o[j] = rr;
+            R.qo[j] = qoffsets(DT, (int64_t)R.g[j].rows * in_dim, a.gs);
+        }
+    };
+    auto issue = [&](const RowGroup<RW> &R, int c0, u32x4 (&w1)[RW][U], u32x4 (&w2)[RW][U]) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int c = min(c0 + u * 64 + lane, chunks - 1);
+#pragma unroll
+            for (int j = 0; j < RW; ++j) {
+                w1[j][u] = stream_load(reinterpret_cast<const u32x4 *>(R.g[j].W + R.o[j] * row_bytes) + c);
+                if constexpr (kTwo)
+                    w2[j][u] = stream_load(reinterpret_cast<const u32x4 *>(R.g[j].W2 + R.o[j] * row_bytes) + c);
+            }
+        }
+    };
+
+    int r0 = (blockIdx.x * kGemvWaves + wave) * RW, c0 = 0;
+    RowGroup<RW> RA, RB;
+    u32x4 wa1[RW][U], wa2[RW][U], wb1[RW][U], wb2[RW][U];
+    if (r0 < a.total_rows) {
+        resolve(r0, RA);
+        issue(RA, 0, wa1, wa2);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
     // Stage x with 16-byte loads, kStageUnroll in flight per thread (in_dim is
     // a multiple of 4: every weight dtype reads at least 4 elements a chunk),
-    // summing the squares on the way; then normalise in place.
+    // summing the squares on the way; then normalise in place.  LDS holds x
+    // as E/4 planes of float4, plane q holding elements 4q .. 4q + 3 of every
+    // chunk: lanes reading consecutive chunks read consecutive 16-byte slots
+    // (no bank conflicts; chunk-major storage conflicts 2-way for bf16 and
+    // more for the quantized dtypes).
     constexpr int kStageUnroll = 8;
     const int n4 = in_dim / 4;
     const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
@@ -223,7 +297,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
         for (int u = 0; u < kStageUnroll; ++u) {
             const int i = i0 + u * 64 * kGemvWaves + threadIdx.x;
             if (i < n4) {
-                xs4[i] = v[u];
+                xs4[(i % (E / 4)) * chunks + i / (E / 4)] = v[u];
                 ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
             }
         }
@@ -236,80 +310,84 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int w = 0; w < kGemvWaves; ++w) tot += red[w];
         const float inv = 1.0f / sqrtf(tot / (float)in_dim + a.eps);
-        for (int i = threadIdx.x; i < in_dim; i += 64 * kGemvWaves)
-            xs[i] = xs[i] * inv * a.norm_w[i];
+        for (int k = threadIdx.x; k < n4; k += 64 * kGemvWaves) {
+            const float *nw = a.norm_w + (k % chunks) * E + 4 * (k / chunks);
+            float4 t = xs4[k];
+            t.x = t.x * inv * nw[0];
+            t.y = t.y * inv * nw[1];
+            t.z = t.z * inv * nw[2];
+            t.w = t.w * inv * nw[3];
+            xs4[k] = t;
+        }
     }
     __syncthreads();
 
-    const int chunks = in_dim / E;
-    const int64_t row_bytes = (int64_t)in_dim * 16 / E;
-    // RW rows per wave at a time, U chunk loads per lane per row per step:
-    // RW * U (x2 for SwiGLU) 16-byte loads in flight whatever the row length.
-    for (int r0 = (blockIdx.x * kGemvWaves + wave) * RW; r0 < a.total_rows;
-         r0 += gridDim.x * kGemvWaves * RW) {
-        GemvSeg g[RW];
-        int o[RW];
-        QOffsets qo[RW];
+    float acc[RW], acc2[RW];
 #pragma unroll
-        for (int j = 0; j < RW; ++j) {
-            // Segment of launch row r0 + j (explicit selects: a dynamically
-            // indexed kernel-argument array would be copied to scratch).  Rows
-            // past the end repeat the last row, and are not stored.
-            int rr = min(r0 + j, a.total_rows - 1);
-            g[j] = a.seg[0];
-            if (a.nseg > 1 && rr >= a.seg[0].rows) {
-                rr -= a.seg[0].rows;
-                g[j] = a.seg[1];
-                if (a.nseg > 2 && rr >= a.seg[1].rows) {
-                    rr -= a.seg[1].rows;
-                    g[j] = a.seg[2];
-                }
-            }
-            o[j] = rr;
-            qo[j] = qoffsets(DT, (int64_t)g[j].rows * in_dim, a.gs);
+    for (int j = 0; j < RW; ++j) acc[j] = acc2[j] = 0.f;
+
+    // One step: issue the next step's loads into (Rn, wn), then consume
+    // (Rc, wc) at (r0, c0); finish the rows after their last chunk block.
+    // Returns false when the wave has no further step.
+    auto step = [&](RowGroup<RW> &Rc, u32x4 (&wc1)[RW][U], u32x4 (&wc2)[RW][U], RowGroup<RW> &Rn,
+                    u32x4 (&wn1)[RW][U], u32x4 (&wn2)[RW][U]) -> bool {
+        int r1 = r0, c1 = c0 + 64 * U;
+        const bool last = c1 >= chunks;
+        if (last) {
+            c1 = 0;
+            r1 += rstride;
         }
-        float acc[RW], acc2[RW];
+        if (r1 < a.total_rows) {
+            resolve(r1, Rn);  // scalar work; a struct copy here defeats SROA
+            issue(Rn, c1, wn1, wn2);
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int j = 0; j < RW; ++j) acc[j] = acc2[j] = 0.f;
-        for (int c0 = 0; c0 < chunks; c0 += 64 * U) {
-            u32x4 w1[RW][U], w2[RW][U];
+        for (int u = 0; u < U; ++u) {
+            const int c = c0 + u * 64 + lane;
+            if (c < chunks) {
+                float xv[E];  // this chunk's x, read once for the RW rows
 #pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = min(c0 + u * 64 + lane, chunks - 1);
+                for (int q = 0; q < E / 4; ++q) {
+                    const float4 t = xs4[q * chunks + c];
+                    xv[4 * q] = t.x;
+                    xv[4 * q + 1] = t.y;
+                    xv[4 * q + 2] = t.z;
+                    xv[4 * q + 3] = t.w;
+                }
 #pragma unroll
                 for (int j = 0; j < RW; ++j) {
-                    w1[j][u] = stream_load(reinterpret_cast<const u32x4 *>(g[j].W + o[j] * row_bytes) + c);
-                    if constexpr (EPI == kSwiGLU)
-                        w2[j][u] = stream_load(reinterpret_cast<const u32x4 *>(g[j].W2 + o[j] * row_bytes) + c);
-                }
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int c = c0 + u * 64 + lane;
-                if (c < chunks) {
-#pragma unroll
-                    for (int j = 0; j < RW; ++j) {
-                        const int64_t i0 = (int64_t)o[j] * in_dim + (int64_t)c * E;
-                        acc[j] += C::dot(w1[j][u], xs + c * E, g[j].W, qo[j].scales, qo[j].zeros, a.gs, i0);
-                        if constexpr (EPI == kSwiGLU)
-                            acc2[j] += C::dot(w2[j][u], xs + c * E, g[j].W2, qo[j].scales, qo[j].zeros, a.gs, i0);
-                    }
+                    const int64_t i0 = (int64_t)Rc.o[j] * in_dim + (int64_t)c * E;
+                    acc[j] += C::dot(wc1[j][u], xv, Rc.g[j].W, Rc.qo[j].scales, Rc.qo[j].zeros, a.gs, i0);
+                    if constexpr (kTwo)
+                        acc2[j] += C::dot(wc2[j][u], xv, Rc.g[j].W2, Rc.qo[j].scales, Rc.qo[j].zeros, a.gs, i0);
                 }
             }
         }
+        if (last) {
 #pragma unroll
-        for (int j = 0; j < RW; ++j) {
-            const float s1 = wave_sum<64>(acc[j]);
-            const float s2 = EPI == kSwiGLU ? wave_sum<64>(acc2[j]) : 0.f;
-            if (lane == 0 && r0 + j < a.total_rows) {
-                if constexpr (EPI == kStoreBias) {
-                    g[j].out[o[j]] = s1 + (g[j].bias ? g[j].bias[o[j]] : 0.f);
-                } else if constexpr (EPI == kAddInto) {
-                    g[j].out[o[j]] = g[j].out[o[j]] + s1;
-                } else {
-                    g[j].out[o[j]] = s1 / (1.0f + expf(-s1)) * s2;  // silu(gate) * up, cpu.rs:960-975
+            for (int j = 0; j < RW; ++j) {
+                const float s1 = wave_sum<64>(acc[j]);
+                const float s2 = kTwo ? wave_sum<64>(acc2[j]) : 0.f;
+                if (lane == 0 && r0 + j < a.total_rows) {
+                    if constexpr (EPI == kStoreBias) {
+                        Rc.g[j].out[Rc.o[j]] = s1 + (Rc.g[j].bias ? Rc.g[j].bias[Rc.o[j]] : 0.f);
+                    } else if constexpr (EPI == kAddInto) {
+                        Rc.g[j].out[Rc.o[j]] = Rc.g[j].out[Rc.o[j]] + s1;
+                    } else {
+                        // silu(gate) * up, cpu.rs:960-975
+                        Rc.g[j].out[Rc.o[j]] = s1 / (1.0f + expf(-s1)) * s2;
+                    }
                 }
+                acc[j] = acc2[j] = 0.f;
             }
+        }
+        r0 = r1;
+        c0 = c1;
+        return r0 < a.total_rows;
+    };
+    if (r0 < a.total_rows) {
+        while (step(RA, wa1, wa2, RB, wb1, wb2) && step(RB, wb1, wb2, RA, wa1, wa2)) {
         }
     }
 }
