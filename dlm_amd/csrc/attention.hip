@@ -41,7 +41,7 @@
 namespace {
 
 constexpr int kBlock = 16;          // tokens per KV block (dlm: src/main.rs:455)
-constexpr int kMinPartition = 256;  // smallest partition of any kernel (sizes the workspace)
+constexpr int kMinPartition = 64;  // smallest partition of any kernel (sizes the workspace)
 constexpr float kLog2e = 1.4426950408889634f;
 
 // Matrix-core kernel shape: waves per work-group, blocks per wave, prefetch
@@ -675,7 +675,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
 //     lane's accumulator is ROWS x (loads) floats summed across the 4 lanes
 //     sharing a dim.
 // ---------------------------------------------------------------------------
-template <int D, int GQA, int NQ, int NW>
+template <int D, int GQA, int NQ, int NW, int P>
 __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ q, float *__restrict__ k_pool,
     float *__restrict__ v_pool, const float *__restrict__ k_new, const float *__restrict__ v_new,
@@ -687,7 +687,6 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
     constexpr int KI = CPL / 4;             // 16-byte loads per lane per block (K and V alike)
     constexpr int CPD = kBlock / X;         // V chunks per dim row of a tile
     constexpr int ROWS = GQA * NQ;
-    constexpr int P = kMinPartition;
     constexpr int BPW = P / kBlock / NW;    // blocks per wave
     constexpr int TILE = D * kBlock;
     static_assert(CPL % 4 == 0 && BPW >= 1, "unsupported geometry");
@@ -995,17 +994,30 @@ int launch_mfma(const Args &a) {
     });
 }
 
-template <int D, int GQA, int NQ>
-int launch_valu(const Args &a) {
-    constexpr int NW = GQA * NQ <= 4 ? 4 : 8;
-    return launch_pair<D>(a, kMinPartition, [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
-        hipLaunchKernelGGL((paged_attn_valu_kernel<D, GQA, NQ, NW>), grid, dim3(NW * 64), 0, a.stream,
+// 256-token partitions, or one block per wave when that grid would not fill
+// the chip: a single decoding sequence (dlmk_decode_block_paged) has num_kv_heads
+// x ctx / 256 work-groups, 64 at the 8B shape and ctx 2048 on 256 compute units.
+constexpr int64_t kValuSmallGrid = 1024;  // work-groups
+
+template <int D, int GQA, int NQ, int NW, int P>
+int launch_valu_p(const Args &a) {
+    static_assert(P >= kMinPartition, "partition below the workspace bound");
+    return launch_pair<D>(a, P, [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
+        hipLaunchKernelGGL((paged_attn_valu_kernel<D, GQA, NQ, NW, P>), grid, dim3(NW * 64), 0, a.stream,
                            a.out, a.out_dtype, static_cast<const float *>(a.q),
                            static_cast<float *>(a.k_pool), static_cast<float *>(a.v_pool),
                            static_cast<const float *>(a.k_new), static_cast<const float *>(a.v_new),
                            a.tables, a.ctx_lens, a.Hq, a.Hkv, a.max_blocks, a.num_blocks,
                            a.scale * kLog2e, max_parts, ws_o, ws_ml);
     });
+}
+
+template <int D, int GQA, int NQ>
+int launch_valu(const Args &a) {
+    constexpr int NW = GQA * NQ <= 4 ? 4 : 8;
+    if ((int64_t)a.B * a.Hkv * parts_for(a.max_blocks, 256) < kValuSmallGrid)
+        return launch_valu_p<D, GQA, NQ, NW, NW * kBlock>(a);
+    return launch_valu_p<D, GQA, NQ, NW, 256>(a);
 }
 
 int unsupported_rows(int gqa, int nq) {

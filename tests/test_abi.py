@@ -71,10 +71,10 @@ def test_argument_errors_before_any_launch(dlmk):
 
 
 def test_workspace_size_formula(dlmk):
-    # One partition (<= 256 tokens) needs no workspace.
-    assert dlmk.dlmk_paged_attention_workspace_size(64, 1, 32, 128, 16, 16) == 0
-    # 4096-token tables: 16 partitions of (d + 2) floats per query row.
-    rows, parts = 64 * 32, 16
+    # One partition (<= 64 tokens, the smallest any kernel uses) needs no workspace.
+    assert dlmk.dlmk_paged_attention_workspace_size(64, 1, 32, 128, 16, 4) == 0
+    # 4096-token tables: 64 partitions of (d + 2) floats per query row.
+    rows, parts = 64 * 32, 64
     o = rows * parts * 128 * 4
     assert dlmk.dlmk_paged_attention_workspace_size(64, 1, 32, 128, 16, 256) == \
         (o + 255) // 256 * 256 + rows * parts * 8
