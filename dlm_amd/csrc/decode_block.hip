@@ -18,9 +18,10 @@
 //                        matrix for SwiGLU) plus the next step's prefetched,
 //                        wave reduction; epilogue = bias store, residual add,
 //                        or (two matrices) SwiGLU; q, k and v as one launch.
-//   rope_append_kernel   RoPE on q and k (NeoX split-half, host-computed
-//                        inv_freq), then the new token's K and V straight into
-//                        the pools at the slot the block table gives; also
+//                        The q/k/v launch's epilogue is RoPE (NeoX split-half,
+//                        host-computed inv_freq) over row pairs of one head,
+//                        with the new token's K and V written straight into
+//                        the pools at the slot the block table gives; it also
 //                        writes the context length the attention reads.
 // Attention is dlmk_paged_decode_attention (f32 pools).
 
@@ -170,7 +171,7 @@ __host__ __device__ inline QOffsets qoffsets(int dt, int64_t n, int64_t gs) {
     return QOffsets{s, s + groups * 4};
 }
 
-enum Epilogue { kStoreBias = 0, kAddInto = 1, kSwiGLU = 2 };
+enum Epilogue { kStoreBias = 0, kAddInto = 1, kSwiGLU = 2, kRopeAppend = 3 };
 
 // Up to three matrices over the same input, as one launch (q, k and v share
 // the normalised hidden state).  A segment's rows follow the previous
@@ -182,12 +183,24 @@ struct GemvSeg {
     int rows;
 };
 
+// kRopeAppend: segments q, k, v (+ biases); q is rotated in place into its
+// output, the rotated k and v go straight into the pools.
+struct RopeArgs {
+    const float *inv_freq;
+    float *k_pool, *v_pool;
+    const int32_t *table;
+    int64_t num_blocks;
+    int num_kv_heads, head_dim, num_positions, position;
+    int32_t *ctx_len;
+};
+
 struct GemvArgs {
     GemvSeg seg[3];
     int nseg, total_rows, in_dim, gs;
     const float *x;
     const float *norm_w;  // non-null: x is staged as rmsnorm(x) * norm_w
     float eps;
+    RopeArgs rope;
 };
 
 // Row-major [rows][in_dim] matrices times x.  Work-group: kGemvWaves waves
@@ -209,9 +222,45 @@ struct GemvArgs {
 template <int RW>
 struct RowGroup {  // RW launch rows resolved to their segments
     GemvSeg g[RW];
-    int o[RW];
+    int o[RW], si[RW];
     QOffsets qo[RW];
 };
+
+// RoPE pair (rope_inplace, src/forward/cpu.rs:1094-1114: NeoX split-half,
+// host-computed inv_freq) of rows `row` (dim i of its head) and row + d/2 of
+// segment si: q rotated into out; k rotated and v as they are into the pools
+// at position num_positions of the sequence (table[p / 16], offset p % 16, f32
+// layouts K [blk][Hkv][d/4][16][4], V [blk][Hkv][d][16]); a block id outside
+// the pool is skipped (the attention masks it).
+__device__ __forceinline__ void rope_store(const RopeArgs &r, int si, float *out, int row, float a,
+                                           float b) {
+    const int d = r.head_dim, half = d / 2, h = row / d, i = row % d;
+    if (si < 2) {
+        const float ang = (float)r.position * r.inv_freq[i];
+        const float sn = sinf(ang), cs = cosf(ang);
+        const float ra = a * cs - b * sn, rb = a * sn + b * cs;
+        a = ra;
+        b = rb;
+    }
+    if (si == 0) {
+        out[row] = a;
+        out[row + half] = b;
+        return;
+    }
+    const int64_t blk = r.table[r.num_positions / kBlock];
+    if (blk < 0 || blk >= r.num_blocks) return;
+    const int t = r.num_positions % kBlock;
+    const int64_t tile = (blk * r.num_kv_heads + h) * (int64_t)d * kBlock;
+    if (si == 1) {
+        float *kt = r.k_pool + tile;
+        kt[((i / 4) * kBlock + t) * 4 + i % 4] = a;
+        kt[(((i + half) / 4) * kBlock + t) * 4 + (i + half) % 4] = b;
+    } else {
+        float *vt = r.v_pool + tile;
+        vt[(int64_t)i * kBlock + t] = a;
+        vt[(int64_t)(i + half) * kBlock + t] = b;
+    }
+}
 
 template <int DT, int EPI, int RW, int U>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
@@ -240,13 +289,22 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
             // past the end repeat the last row, and are not stored.
             int rr = min(r0 + j, a.total_rows - 1);
             R.g[j] = a.seg[0];
+            R.si[j] = 0;
             if (a.nseg > 1 && rr >= a.seg[0].rows) {
                 rr -= a.seg[0].rows;
                 R.g[j] = a.seg[1];
+                R.si[j] = 1;
                 if (a.nseg > 2 && rr >= a.seg[1].rows) {
                     rr -= a.seg[1].rows;
                     R.g[j] = a.seg[2];
+                    R.si[j] = 2;
                 }
+            }
+            if constexpr (EPI == kRopeAppend) {
+                // Launch rows 2p, 2p + 1 are rows i and i + d/2 of one head
+                // (p = head * d/2 + i): the RoPE pair lands in one wave.
+                const int half = a.rope.head_dim / 2, pr = rr >> 1;
+                rr = (pr / half) * a.rope.head_dim + pr % half + (rr & 1) * half;
             }
             R.o[j] = rr;
             R.qo[j] = qoffsets(DT, (int64_t)R.g[j].rows * in_dim, a.gs);
@@ -265,6 +323,8 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
         }
     };
 
+    if constexpr (EPI == kRopeAppend)
+        if (blockIdx.x == 0 && threadIdx.x == 0) *a.rope.ctx_len = a.rope.num_positions + 1;
     int r0 = (blockIdx.x * kGemvWaves + wave) * RW, c0 = 0;
     RowGroup<RW> RA, RB;
     u32x4 wa1[RW][U], wa2[RW][U], wb1[RW][U], wb2[RW][U];
@@ -364,7 +424,19 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
                 }
             }
         }
-        if (last) {
+        if constexpr (EPI == kRopeAppend) {
+            static_assert(RW == 2, "RoPE pairs need two rows per wave");
+            if (last) {
+                float s[2];
+#pragma unroll
+                for (int j = 0; j < 2; ++j) {
+                    s[j] = wave_sum<64>(acc[j]);
+                    if (Rc.g[j].bias) s[j] += Rc.g[j].bias[Rc.o[j]];
+                    acc[j] = acc2[j] = 0.f;
+                }
+                if (lane == 0 && r0 < a.total_rows) rope_store(a.rope, Rc.si[0], Rc.g[0].out, Rc.o[0], s[0], s[1]);
+            }
+        } else if (last) {
 #pragma unroll
             for (int j = 0; j < RW; ++j) {
                 const float s1 = wave_sum<64>(acc[j]);
@@ -392,50 +464,6 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     }
 }
 
-// ---------------------------------------------------------------------------
-// RoPE (rope_inplace, src/forward/cpu.rs:1094-1114) on q in place and on k,
-// then the token's K (rotated) and V go to position num_positions of the
-// sequence: block table[p / 16], offset p % 16, in the f32 pool layouts
-// K [blk][Hkv][d/4][16][4], V [blk][Hkv][d][16].  A block id outside the pool
-// is skipped (the attention masks it).  Thread 0 writes the context length.
-// ---------------------------------------------------------------------------
-__global__ void rope_append_kernel(float *__restrict__ q, const float *__restrict__ k,
-                                   const float *__restrict__ v, const float *__restrict__ inv_freq,
-                                   float *__restrict__ k_pool, float *__restrict__ v_pool,
-                                   const int32_t *__restrict__ table, int64_t num_blocks,
-                                   int num_heads, int num_kv_heads, int head_dim, int num_positions,
-                                   int position, int32_t *__restrict__ ctx_len) {
-    const int half = head_dim / 2;
-    const int nq = num_heads * half, nk = num_kv_heads * half, nv = num_kv_heads * head_dim;
-    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
-    if (idx == 0) *ctx_len = num_positions + 1;
-    const int64_t blk = table[num_positions / kBlock];
-    const int t = num_positions % kBlock;
-    const bool in_pool = blk >= 0 && blk < num_blocks;
-    const int64_t tile = (int64_t)head_dim * kBlock;
-    if (idx < nq + nk) {
-        const bool is_q = idx < nq;
-        const int r = is_q ? idx : idx - nq;
-        const int h = r / half, i = r % half;
-        const float ang = (float)position * inv_freq[i];
-        const float sn = sinf(ang), cs = cosf(ang);
-        const float *src = is_q ? q : k;
-        const float a = src[h * head_dim + i], b = src[h * head_dim + i + half];
-        const float ra = a * cs - b * sn, rb = a * sn + b * cs;
-        if (is_q) {
-            q[h * head_dim + i] = ra;
-            q[h * head_dim + i + half] = rb;
-        } else if (in_pool) {
-            float *kt = k_pool + (blk * num_kv_heads + h) * tile;
-            kt[((i / 4) * kBlock + t) * 4 + i % 4] = ra;
-            kt[(((i + half) / 4) * kBlock + t) * 4 + (i + half) % 4] = rb;
-        }
-    } else if (idx < nq + nk + nv && in_pool) {
-        const int r = idx - nq - nk;
-        const int h = r / head_dim, j = r % head_dim;
-        v_pool[(blk * num_kv_heads + h) * tile + (int64_t)j * kBlock + t] = v[r];
-    }
-}
 
 int w_elems_per_chunk(int dt) {
     switch (dt) {
@@ -485,13 +513,17 @@ void launch_gemv_rw(hipStream_t st, const GemvArgs &a) {
 template <int DT, int EPI>
 void launch_gemv_epi(hipStream_t st, const GemvArgs &a) {
     constexpr int T = EPI == kSwiGLU ? 8 : 16;
-    const int per_lane = (a.in_dim / WChunk<DT>::E + 63) / 64;  // chunk loads per lane per row
-    if (per_lane >= T)
-        launch_gemv_rw<DT, EPI, 1, T>(st, a);
-    else if (per_lane >= T / 2)
-        launch_gemv_rw<DT, EPI, 2, T / 2>(st, a);
-    else
-        launch_gemv_rw<DT, EPI, 4, T / 4>(st, a);
+    if constexpr (EPI == kRopeAppend) {
+        launch_gemv_rw<DT, EPI, 2, T / 2>(st, a);  // RoPE pairs: two rows per wave
+    } else {
+        const int per_lane = (a.in_dim / WChunk<DT>::E + 63) / 64;  // chunk loads per lane per row
+        if (per_lane >= T)
+            launch_gemv_rw<DT, EPI, 1, T>(st, a);
+        else if (per_lane >= T / 2)
+            launch_gemv_rw<DT, EPI, 2, T / 2>(st, a);
+        else
+            launch_gemv_rw<DT, EPI, 4, T / 4>(st, a);
+    }
 }
 
 template <int DT>
@@ -500,8 +532,10 @@ void launch_gemv(int epi, hipStream_t st, const GemvArgs &a) {
         launch_gemv_epi<DT, kStoreBias>(st, a);
     else if (epi == kAddInto)
         launch_gemv_epi<DT, kAddInto>(st, a);
-    else
+    else if (epi == kSwiGLU)
         launch_gemv_epi<DT, kSwiGLU>(st, a);
+    else
+        launch_gemv_epi<DT, kRopeAppend>(st, a);
 }
 
 void gemv(int dt, int epi, hipStream_t st, const GemvArgs &a) {
@@ -620,12 +654,11 @@ int dlmk_decode_block_paged(
     add_seg(qkv, q_proj, nullptr, q_bias, q, q_dim);
     add_seg(qkv, k_proj, nullptr, k_bias, k, kv_dim);
     add_seg(qkv, v_proj, nullptr, v_bias, v, kv_dim);
-    gemv(w_dtype, kStoreBias, st, qkv);
-    const int rope_threads = (num_heads + num_kv_heads) * (head_dim / 2) + kv_dim;
-    hipLaunchKernelGGL(rope_append_kernel, dim3((rope_threads + 255) / 256), dim3(256), 0, st, q,
-                       k, v, inv_freq, static_cast<float *>(k_pool), static_cast<float *>(v_pool),
-                       block_table, num_blocks, num_heads, num_kv_heads, head_dim, num_positions,
-                       position, ctx_len);
+    // RoPE and the append are the launch's epilogue (rows paired per head).
+    qkv.rope = RopeArgs{inv_freq, static_cast<float *>(k_pool), static_cast<float *>(v_pool),
+                        block_table, num_blocks, num_kv_heads, head_dim, num_positions, position,
+                        ctx_len};
+    gemv(w_dtype, kRopeAppend, st, qkv);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return dlmk::fail((int)e, "%s launch: %s", who, hipGetErrorString(e));
     const int rc = dlmk_paged_decode_attention(
