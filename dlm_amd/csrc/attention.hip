@@ -474,7 +474,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     }
 
     float m = -INFINITY, lsum = 0.f;
-    float psum = 0.f;  // quantized pools: sum of this lane's P operand (row n)
+    f32x4 accp = {0.f, 0.f, 0.f, 0.f};  // quantized pools: P row sums (rows 4g + j)
     f32x4 acc[VN];
 #pragma unroll
     for (int k = 0; k < VN; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -568,10 +568,21 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
 #pragma unroll
                 for (int j = 0; j < 4; ++j) c[j] = fmaf(-C::kBiasK, qsum, c[j]) * ksc[b][j];
             }
+            // Every row sees all 16 tokens of this block (all blocks but a
+            // sequence's last, for one query): no masking (wave-uniform).
+            // Quantized pools only: the f16 kernel is memory-bound and
+            // measured 0.3 points slower with the branch.
+            const bool full = C::kScaled && __builtin_amdgcn_readfirstlane(
+                ok[b] && (lbs[b] + 1) * kBlock <= ctx - NQ + 1);
+            if (full) {
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const int pos = lbs[b] * kBlock + 4 * g + j;
-                s[b][j] = (ok[b] && pos < limit) ? c[j] * scale_log2 : -INFINITY;
+                for (int j = 0; j < 4; ++j) s[b][j] = c[j] * scale_log2;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int pos = lbs[b] * kBlock + 4 * g + j;
+                    s[b][j] = (ok[b] && pos < limit) ? c[j] * scale_log2 : -INFINITY;
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -602,7 +613,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
                 const float p = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[b][j] - m);
                 if constexpr (C::kScaled) {
                     // p is 0 there already; the select keeps a NaN scale out.
-                    pa[j] = (PT)(4 * g + j < valid ? p * vsc[b][j] : 0.f);
+                    pa[j] = (PT)(valid >= kBlock || 4 * g + j < valid ? p * vsc[b][j] : 0.f);
                     lsum += p;
                 } else {
                     const PT ph = (PT)p;
@@ -611,11 +622,13 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
                 }
             }
             if constexpr (C::kScaled) {
-                // Exact sum of the operand the MFMA sees, subnormals included
-                // (v_dot2_f32_f16 is not: the bias turns any difference into
-                // kBias times that much output error).
-#pragma unroll
-                for (int j = 0; j < 4; ++j) psum += (float)pa[j];
+                // Row sums of the operand the MFMA sees, subnormals included,
+                // on the matrix pipe: P . ones leaves row 4g + j's sum in
+                // column n of accp[j] (v_dot2_f32_f16 flushes subnormal f16
+                // and the bias turns any difference into kBias times that
+                // much output error).
+                const x4 ones = {(PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f};
+                accp = M::pv(pa, ones, accp);
             }
             typename M::x4 vo[VN];
 #pragma unroll
@@ -639,12 +652,10 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     lsum += __shfl_xor(lsum, 16);
     lsum += __shfl_xor(lsum, 32);
     if constexpr (C::kScaled) {
-        // Output bias of row 4g + j: kBias * (row's P sum), held by lane 4g + j.
-        psum += __shfl_xor(psum, 16);
-        psum += __shfl_xor(psum, 32);
+        // Output bias of row 4g + j: kBias * (row's P sum).
         float ob[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) ob[j] = C::kBias * __shfl(psum, 4 * g + j);
+        for (int j = 0; j < 4; ++j) ob[j] = C::kBias * accp[j];
 #pragma unroll
         for (int k = 0; k < VN; ++k)
 #pragma unroll
