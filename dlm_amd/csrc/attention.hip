@@ -233,9 +233,9 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Exact widening of small integer codes to f16 without conversions: the f16
-// with bit pattern 0x64uu is 1024 + uu for any byte uu, so a code c biased to
-// the unsigned byte c + b and placed under a 0x64 high byte is the f16 value
-// B + c with B = 1024 + b.  v_perm_b32 builds two such halves from bytes lo,
+// with bit pattern 0x64uu is 1024 + uu for any byte uu, so a code c stored
+// offset binary as the unsigned byte (or nibble) c + b and placed under a
+// 0x64 high byte is the f16 value B + c with B = 1024 + b.  v_perm_b32 builds two such halves from bytes lo,
 // lo + 1 of w in one op.  The bias is not subtracted per element: the kernel
 // removes B * sum(q) from each score and B * sum(p) from each output row
 // (dot products are linear in the codes), which takes one VALU op per code
@@ -317,8 +317,8 @@ struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
     using KRaw = u32x4;
     using VRaw = u32x4;
     static constexpr bool kScaled = true;
-    static constexpr float kBias = 1024.f + 128.f, kBiasK = kBias;
-    static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;  // codes stored as c, widened from c + 128
+    static constexpr float kBias = 1024.f + 128.f, kBiasK = kBias;  // bytes c + 128
+    static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;
     static constexpr int64_t kTileBytes = (int64_t)D * kBlock;
     static constexpr int SK = 2, KL = D / 64, SV = 4, VL = D / 64;
     static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int p, int lane) {
@@ -330,10 +330,10 @@ struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
     static __device__ __forceinline__ int q_chunk(int i, int g) { return 8 * (i >> 1) + 2 * g + (i & 1); }
     static __device__ __forceinline__ f16x8 q_op(f16x8 q) { return q; }
     static __device__ __forceinline__ f16x8 k_op(KRaw r, int s) {
-        const f16x4 a = biased4(r[2 * s] ^ 0x80808080u), b = biased4(r[2 * s + 1] ^ 0x80808080u);
+        const f16x4 a = biased4(r[2 * s]), b = biased4(r[2 * s + 1]);
         return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     }
-    static __device__ __forceinline__ f16x4 v_op(VRaw r, int kk) { return biased4(r[kk] ^ 0x80808080u); }
+    static __device__ __forceinline__ f16x4 v_op(VRaw r, int kk) { return biased4(r[kk]); }
     static __device__ __forceinline__ int v_dim(int k, int n) { return 64 * (k >> 2) + 4 * n + (k & 3); }
 };
 
@@ -350,8 +350,8 @@ struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 
     // bias of 1032 the f32 cancellation in the scores, scaled by a large
     // token's K scale, reaches the output tolerance.  V keeps the bias (its
     // error is relative to p * v_scale, which the output is divided by).
-    static constexpr float kBias = 1024.f + 8.f, kBiasK = 0.f;
-    static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;  // nibbles c widened from c + 8
+    static constexpr float kBias = 1024.f + 8.f, kBiasK = 0.f;  // nibbles c + 8
+    static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;
     static constexpr int64_t kTileBytes = (int64_t)D * kBlock / 2;
     static constexpr int SK = KG / 8, KL = D / (4 * KG), SV = VG, VL = D / (16 * VG);
     static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int p, int lane) {
@@ -366,14 +366,14 @@ struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 
         return f16x8{q[0], q[2], q[4], q[6], q[1], q[3], q[5], q[7]};
     }
     static __device__ __forceinline__ f16x8 k_op(KRaw r, int s) {
-        const uint32_t x = r[s] ^ 0x88888888u;  // signed nibble c -> c + 8
+        const uint32_t x = r[s];  // nibbles c + 8
         const f16x4 a = biased4(x & 0x0f0f0f0fu), b = biased4((x >> 4) & 0x0f0f0f0fu);
         const f16x8 w = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
         return w - (_Float16)kBias;
     }
     // Word kk / 2 holds dims kk & ~1 (low nibbles) and kk | 1 of 4 tokens.
     static __device__ __forceinline__ f16x4 v_op(VRaw r, int kk) {
-        return biased4(((r[kk >> 1] >> (4 * (kk & 1))) & 0x0f0f0f0fu) ^ 0x08080808u);
+        return biased4((r[kk >> 1] >> (4 * (kk & 1))) & 0x0f0f0f0fu);
     }
     static __device__ __forceinline__ int v_dim(int k, int n) { return 16 * VG * (k / VG) + VG * n + k % VG; }
 };

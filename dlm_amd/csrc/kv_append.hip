@@ -88,6 +88,8 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 //   V [d/(16 VG)][4 token quads][16][VG dims][4 tokens], VG = 4 (int8) or
 //     8 / 4 (int4): one byte per dim (int8) or per dim pair (int4, low nibble
 //     the even dim, so a byte never mixes tokens and appends never share one).
+// Codes are stored offset binary (int8 c as the byte c + 128, int4 c as the
+// nibble c + 8), so the attention kernel widens them without a sign flip.
 template <typename S>
 __device__ __forceinline__ void load8(const S *p, float (&x)[8]) {
     if constexpr (sizeof(S) == 4) {
@@ -165,7 +167,8 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
             uint8_t *tile = pool + (blk * num_kv_heads + h) * tile_bytes;
             int q[8];
 #pragma unroll
-            for (int k = 0; k < 8; ++k) q[k] = quant_code(x[i][k], ok, scale, qmax);
+            // Offset binary in the pools: code c is stored as c + 128 (c + 8).
+            for (int k = 0; k < 8; ++k) q[k] = quant_code(x[i][k], ok, scale, qmax) + (QBITS == 8 ? 128 : 8);
             // V: dim jj of this token sits at lane group (jj / VG) % 16 of
             // quarter jj / (16 VG), word (jj % VG) / (dims per byte), byte t % 4.
             const int vq = j / (16 * VG), vn = (j % (16 * VG)) / VG, vk = j % VG;

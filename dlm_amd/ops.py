@@ -270,7 +270,7 @@ class QuantKv:
 def alloc_quant_pools(num_blocks: int, num_kv_heads: int, head_dim: int, quant: str,
                       device="cuda", block_size: int = BLOCK_SIZE) -> QuantKv:
     """Allocate one layer's int8 / int4 pools in the library's layout (head_dim
-    a multiple of 64; int4 codes two to a byte):
+    a multiple of 64; codes offset binary, c + 128 / c + 8, int4 two to a byte):
     K [nb, Hkv, d/KG, 16, KG], V [nb, Hkv, d/(16 VG), 4, 16, 4 VG] with KG, VG =
     16, 4 for int8 and 32, 8 (d % 128 == 0) or 16, 4 for int4; scales [nb, 16]
     float32 (zero)."""

@@ -238,8 +238,9 @@ int dlmk_paged_decode_step(void *stream, void *out, int out_dtype, const void *q
  * its whole kv_dim (num_kv_heads * head_dim values): scale = max|x| / qmax
  * (qmax 127 / 7), code = round-half-away(x / scale) clamped to +-qmax, and an
  * all-zero token has scale 0 and zero codes.  head_dim is a multiple of 64.
- * Layouts per layer (block_size 16), int4 codes two to a byte (low nibble
- * the even element), each (block, kv head) tile:
+ * Codes are stored offset binary: int8 code c as the byte c + 128, int4 code
+ * c as the nibble c + 8, two to a byte (low nibble the even element).
+ * Layouts per layer (block_size 16), each (block, kv head) tile:
  *   K [d/KG][16 tokens][KG dims]: KG = 16 (int8); int4 KG = 32 if
  *     d % 128 == 0, else 16.
  *   V [d/(16 VG)][4 token quads][16][VG dims][4 tokens]: VG = 4 (int8);

@@ -620,7 +620,8 @@ void orc_quantize_tokens(const float *src, int64_t n_tok, int64_t kv_dim, int qu
 
 /* Paged quantized pools (layout of this build, no reference counterpart).
  * head_dim d is a multiple of 64.  Elements are 8-bit codes (int8) or 4-bit
- * codes two to a byte (int4, low nibble the even element).
+ * codes two to a byte (int4, low nibble the even element), stored offset
+ * binary: the byte c + 128, the nibble c + 8.
  *   K tile of one (block, kv head): [d/KG][16 tokens][KG dims], KG = 16
  *     (int8) or, for int4, 32 when d % 128 == 0 else 16 -- one token's KG
  *     consecutive dims fill 16 bytes (8 for int4 at d = 64).
@@ -633,9 +634,20 @@ static void put_nibble(uint8_t *b, int hi, int code) {
     uint8_t nib = (uint8_t)code & 0x0f;
     *b = hi ? (uint8_t)((*b & 0x0f) | (nib << 4)) : (uint8_t)((*b & 0xf0) | nib);
 }
-static int get_nibble(const uint8_t *b, int hi) {
-    int nib = hi ? (*b >> 4) : (*b & 0x0f);
-    return nib >= 8 ? nib - 16 : nib;
+/* Pool codes are offset binary: int8 code c is the byte c + 128, int4 code c
+ * the nibble c + 8 (the contiguous reference rows stay two's complement). */
+static void pool_put(void *pool, int64_t off, int hi, int code, int quant) {
+    if (quant == ORC_I8) {
+        ((uint8_t *)pool)[off] = (uint8_t)(code + 128);
+        return;
+    }
+    uint8_t *b = (uint8_t *)pool + off, nib = (uint8_t)(code + 8) & 0x0f;
+    *b = hi ? (uint8_t)((*b & 0x0f) | (nib << 4)) : (uint8_t)((*b & 0xf0) | nib);
+}
+static int pool_get(const void *pool, int64_t off, int hi, int quant) {
+    const uint8_t b = ((const uint8_t *)pool)[off];
+    if (quant == ORC_I8) return (int)b - 128;
+    return (int)(hi ? (b >> 4) : (b & 0x0f)) - 8;
 }
 
 int orc_quant_k_group(int d, int quant) { return quant == ORC_I8 ? 16 : (d % 128 == 0 ? 32 : 16); }
@@ -680,13 +692,8 @@ void orc_paged_append_quant(void *k_pool, void *v_pool, float *k_scales, float *
                 int kq = (int)quant_code(kc, 0, e, quant), vq = (int)quant_code(vc, 0, e, quant);
                 int64_t ko = qk_off(blk, h, t, j, Hkv, d, quant);
                 int64_t vo = qv_off(blk, h, t, j, Hkv, d, quant);
-                if (quant == ORC_I8) {
-                    ((int8_t *)k_pool)[ko] = (int8_t)kq;
-                    ((int8_t *)v_pool)[vo] = (int8_t)vq;
-                } else {
-                    put_nibble((uint8_t *)k_pool + ko, j % 2, kq);
-                    put_nibble((uint8_t *)v_pool + vo, j % 2, vq);
-                }
+                pool_put(k_pool, ko, j % 2, kq, quant);
+                pool_put(v_pool, vo, j % 2, vq, quant);
             }
     }
     free(kc);
@@ -713,13 +720,13 @@ void orc_paged_gather_quant(const void *k_pool, const void *v_pool, const float 
                 int64_t ko = qk_off(blk, h, t, j, Hkv, d, quant);
                 int64_t vo = qv_off(blk, h, t, j, Hkv, d, quant);
                 if (quant == ORC_I8) {
-                    ((int8_t *)kcodes)[p * rb + e] = ((const int8_t *)k_pool)[ko];
-                    ((int8_t *)vcodes)[p * rb + e] = ((const int8_t *)v_pool)[vo];
+                    ((int8_t *)kcodes)[p * rb + e] = (int8_t)pool_get(k_pool, ko, 0, quant);
+                    ((int8_t *)vcodes)[p * rb + e] = (int8_t)pool_get(v_pool, vo, 0, quant);
                 } else {
                     uint8_t *kb = (uint8_t *)kcodes + p * rb + e / 2;
                     uint8_t *vb = (uint8_t *)vcodes + p * rb + e / 2;
-                    put_nibble(kb, (int)(e % 2), get_nibble((const uint8_t *)k_pool + ko, j % 2));
-                    put_nibble(vb, (int)(e % 2), get_nibble((const uint8_t *)v_pool + vo, j % 2));
+                    put_nibble(kb, (int)(e % 2), pool_get(k_pool, ko, j % 2, quant));
+                    put_nibble(vb, (int)(e % 2), pool_get(v_pool, vo, j % 2, quant));
                 }
             }
     }

@@ -380,10 +380,11 @@ def _unpack_codes(c, quant):
 
 
 def _pack_tile_codes(vals, quant):
-    """Signed values whose last axis runs over consecutive elements -> bytes."""
+    """Signed codes whose last axis runs over consecutive elements -> pool bytes
+    (offset binary: the byte c + 128, the nibble c + 8)."""
     if quant == 3:
-        return vals.astype(np.int8).view(np.uint8)
-    u = (vals & 15).astype(np.uint8)
+        return (vals + 128).astype(np.uint8)
+    u = (vals + 8).astype(np.uint8)
     return u[..., 0::2] | (u[..., 1::2] << 4)
 
 
@@ -392,7 +393,7 @@ def _pack_tile_codes(vals, quant):
 def test_paged_quant_layout_by_axes(oracle, quant, d):
     """The paged quantized layout, restated as numpy axis permutations of the
     [token][head][dim] codes and compared with the oracle's append byte for
-    byte over one full block per head:
+    byte over one full block per head, codes stored offset binary:
       K [d/KG][16 tokens][KG dims];  V [d/(16 VG)][4 quads][16][VG dims][4 tokens],
     with KG, VG = 16, 4 (int8) and 32, 8 or 16, 4 (int4, d % 128 == 0 or not)."""
     Hkv, bs = 2, 16
