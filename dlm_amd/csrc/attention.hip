@@ -50,7 +50,7 @@ constexpr float kLog2e = 1.4426950408889634f;
 #define DLMK_MFMA_NW 4
 #endif
 #ifndef DLMK_MFMA_NB
-#define DLMK_MFMA_NB 8
+#define DLMK_MFMA_NB 16
 #endif
 #ifndef DLMK_MFMA_PD
 #define DLMK_MFMA_PD 2

@@ -166,7 +166,7 @@ def quant_workload(oracle, rng, ctx, Hkv, d, quant):
 @pytest.mark.parametrize("qname", ["int8", "int4"])
 @pytest.mark.parametrize("ctx,Hq,Hkv,d,nq", [
     ([1, 17, 300, 64], 32, 8, 64, 1),        # config-1 heads, ragged
-    ([700, 1, 1300, 513], 32, 8, 128, 1),    # split over 512-token partitions
+    ([700, 1, 1300, 513, 2100], 32, 8, 128, 1),  # split over 1024-token partitions
     ([2100, 45], 64, 8, 128, 1),             # GQA 8
     ([600, 4, 90], 16, 4, 128, 4),           # 4-query verify
     ([777, 16], 32, 2, 256, 1),              # GQA 16, d 256
