@@ -894,51 +894,85 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_kernel(
     int max_blocks, int partition, int max_parts) {
     constexpr int W = kCombineWaves;
     constexpr int DPL = D / 64;  // dims per lane
-    __shared__ float red[W];
+    __shared__ float wml[W][2];
     __shared__ float so[W][D + 1];
     const int seq = blockIdx.y;
-    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
-    const int nparts = parts_of(ctx, partition);
-    if (nparts == 1) return;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t row = (int64_t)seq * rows_per_seq + blockIdx.x;
     const float *ml = ws_ml + 2 * row * max_parts;
     const float *o = ws_o + row * max_parts * D;
 
-    float M = -INFINITY;
-    for (int p = threadIdx.x; p < nparts; p += 64 * W) M = fmaxf(M, ml[2 * p]);
-    M = xor_max<64>(M);
-    if (lane == 0) red[wave] = M;
-    __syncthreads();
-    M = red[0];
+    // Wave w's first partition (w) is loaded before the context length is
+    // known (the slot exists for every w < max_parts; it is used only if
+    // w < nparts), so the common case -- at most W partitions -- costs one
+    // memory round trip.  Further partitions w + W, ... fold in with an
+    // online rescale; the W waves then merge once.
+    float m = -INFINITY, L = 0.f, O[DPL];
+    float m0 = -INFINITY, l0 = 0.f, o0[DPL];
 #pragma unroll
-    for (int w = 1; w < W; ++w) M = fmaxf(M, red[w]);
-
-    float O[DPL], L = 0.f;
+    for (int k = 0; k < DPL; ++k) O[k] = o0[k] = 0.f;
+    if (wave < max_parts) {
+        m0 = ml[2 * wave];
+        l0 = ml[2 * wave + 1];
 #pragma unroll
-    for (int k = 0; k < DPL; ++k) O[k] = 0.f;
-    if (M != -INFINITY) {
-#pragma unroll 4
-        for (int p = wave; p < nparts; p += W) {
-            const float mp = ml[2 * p];
-            const float f = mp == -INFINITY ? 0.f : exp2f(mp - M);
-            L = fmaf(f, ml[2 * p + 1], L);
+        for (int k = 0; k < DPL; ++k) o0[k] = o[(int64_t)wave * D + lane + 64 * k];
+    }
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    const int nparts = parts_of(ctx, partition);
+    if (nparts == 1) return;
+    if (wave < nparts) {
+        m = m0;
+        L = l0;
 #pragma unroll
-            for (int k = 0; k < DPL; ++k) O[k] = fmaf(f, o[(int64_t)p * D + lane + 64 * k], O[k]);
+        for (int k = 0; k < DPL; ++k) O[k] = o0[k];
+    }
+    // Later partitions in batches of B per wave: all of a batch's loads go
+    // out before any is folded (indices clamped into the row, folds skipped
+    // past nparts).
+    constexpr int B = 8;
+    for (int p0 = wave + W; p0 < nparts; p0 += B * W) {
+        float mb[B], lb[B], ob[B][DPL];
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int p = min(p0 + i * W, nparts - 1);
+            mb[i] = ml[2 * p];
+            lb[i] = ml[2 * p + 1];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) ob[i][k] = o[(int64_t)p * D + lane + 64 * k];
+        }
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            if (p0 + i * W >= nparts) break;
+            const float mn = fmaxf(m, mb[i]);
+            if (mn == -INFINITY) continue;  // both empty
+            const float fa = m == -INFINITY ? 0.f : exp2f(m - mn);
+            const float fb = mb[i] == -INFINITY ? 0.f : exp2f(mb[i] - mn);
+            L = fa * L + fb * lb[i];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) O[k] = fa * O[k] + fb * ob[i][k];
+            m = mn;
         }
     }
-    __syncthreads();  // red[] reads done before it is reused for L
 #pragma unroll
     for (int k = 0; k < DPL; ++k) so[wave][lane + 64 * k] = O[k];
-    if (lane == 0) red[wave] = L;
+    if (lane == 0) {
+        wml[wave][0] = m;
+        wml[wave][1] = L;
+    }
     __syncthreads();
-    float Lt = 0.f;
+    float M = -INFINITY;
 #pragma unroll
-    for (int w = 0; w < W; ++w) Lt += red[w];
+    for (int w = 0; w < W; ++w) M = fmaxf(M, wml[w][0]);
+    float fw[W], Lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        fw[w] = (M == -INFINITY || wml[w][0] == -INFINITY) ? 0.f : exp2f(wml[w][0] - M);
+        Lt = fmaf(fw[w], wml[w][1], Lt);
+    }
     for (int d = threadIdx.x; d < D; d += 64 * W) {
         float Ot = 0.f;
 #pragma unroll
-        for (int w = 0; w < W; ++w) Ot += so[w][d];
+        for (int w = 0; w < W; ++w) Ot = fmaf(fw[w], so[w][d], Ot);
         store_out(out, out_dtype, row * D + d, Lt > 0.f ? Ot / Lt : 0.f);
     }
 }
