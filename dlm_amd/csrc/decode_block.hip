@@ -345,6 +345,20 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     const int n4 = in_dim / 4;
     const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
     float4 *xs4 = reinterpret_cast<float4 *>(xs);
+    // The norm weights of this thread's first kNormPre normalise-pass slots,
+    // loaded with x (not after the reduction's barrier).
+    constexpr int kNormPre = 4;
+    float4 nwv[kNormPre];
+    if (a.norm_w != nullptr) {
+#pragma unroll
+        for (int j = 0; j < kNormPre; ++j) {
+            const int k = threadIdx.x + j * 64 * kGemvWaves;
+            if (k < n4) {
+                const float *nw = a.norm_w + (k % chunks) * E + 4 * (k / chunks);
+                nwv[j] = make_float4(nw[0], nw[1], nw[2], nw[3]);
+            }
+        }
+    }
     float ss = 0.f;
     for (int i0 = 0; i0 < n4; i0 += 64 * kGemvWaves * kStageUnroll) {
         float4 v[kStageUnroll];
@@ -370,14 +384,22 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
 #pragma unroll
         for (int w = 0; w < kGemvWaves; ++w) tot += red[w];
         const float inv = 1.0f / sqrtf(tot / (float)in_dim + a.eps);
-        for (int k = threadIdx.x; k < n4; k += 64 * kGemvWaves) {
-            const float *nw = a.norm_w + (k % chunks) * E + 4 * (k / chunks);
+        auto norm4 = [&](int k, float4 w) {
             float4 t = xs4[k];
-            t.x = t.x * inv * nw[0];
-            t.y = t.y * inv * nw[1];
-            t.z = t.z * inv * nw[2];
-            t.w = t.w * inv * nw[3];
+            t.x = t.x * inv * w.x;
+            t.y = t.y * inv * w.y;
+            t.z = t.z * inv * w.z;
+            t.w = t.w * inv * w.w;
             xs4[k] = t;
+        };
+#pragma unroll
+        for (int j = 0; j < kNormPre; ++j) {
+            const int k = threadIdx.x + j * 64 * kGemvWaves;
+            if (k < n4) norm4(k, nwv[j]);
+        }
+        for (int k = threadIdx.x + kNormPre * 64 * kGemvWaves; k < n4; k += 64 * kGemvWaves) {
+            const float *nw = a.norm_w + (k % chunks) * E + 4 * (k / chunks);
+            norm4(k, make_float4(nw[0], nw[1], nw[2], nw[3]));
         }
     }
     __syncthreads();
