@@ -717,20 +717,27 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
     // peak over first-index-first at the 8B shape).
     const int part = gridDim.y - 1 - blockIdx.y, kvh = blockIdx.x % num_kv_heads,
               seq = blockIdx.x / num_kv_heads;
-    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
-    const int nparts = parts_of(ctx, P);
-    if (part >= nparts) return;
-
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nblk_seq = (ctx + kBlock - 1) / kBlock;
     const int first_lb = part * (P / kBlock) + wave * BPW;
     const int32_t *table = block_tables + (int64_t)seq * max_blocks;
-
-    int64_t blk[BPW];
+    // The table entries are read before the length (indices clamped into the
+    // row, not to the context), so the two reads overlap; entries past the
+    // context are masked below.
     int32_t raw[BPW];
 #pragma unroll
-    for (int b = 0; b < BPW; ++b) raw[b] = table[max(min(first_lb + b, nblk_seq - 1), 0)];
+    for (int b = 0; b < BPW; ++b) raw[b] = table[min(first_lb + b, max_blocks - 1)];
+    const int len = ctx_lens[seq];
+    // Both reads are used here, so the compiler issues them together and
+    // cannot sink the table reads past the early exit below.
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) asm volatile("" ::"s"(raw[b]), "s"(len));
+    const int ctx = min(len, max_blocks * kBlock);
+    const int nparts = parts_of(ctx, P);
+    if (part >= nparts) return;
+    const int nblk_seq = (ctx + kBlock - 1) / kBlock;
+
+    int64_t blk[BPW];
 #pragma unroll
     for (int b = 0; b < BPW; ++b) {
         const int lb = first_lb + b;
