@@ -34,6 +34,7 @@ def ops(cuda):
     (np.float16, 8, 128, 64, False),  # config-2 shape decode step
     (np.float16, 8, 128, 2096, True), # config-3 step: 48 decode + 4 x 512 chunk
     (np.float16, 2, 64, 300, True),
+    (np.float16, 2, 24, 50, True),    # 3 chunks per head row: one chunk per thread
     ("bf16", 8, 128, 100, False),
 ])
 def test_kv_append_bit_exact(oracle, torch_mod, ops, cuda, dtype, Hkv, d, ntok, chunked):
