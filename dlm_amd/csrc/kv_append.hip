@@ -144,24 +144,33 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
     const int KG = QBITS == 8 ? 16 : (d % 128 == 0 ? 32 : 16);
     const int VG = QBITS == 8 ? 4 : (d % 128 == 0 ? 8 : 4);
     const int VLANE = VG * QBITS / 2;
+    // K's and V's source chunks are loaded together, before any pool store
+    // (the stores could alias the sources as far as the compiler knows, so
+    // V's loads would otherwise wait for K's stores).
+    float xkv[2][NC][8];
 #pragma unroll
     for (int which = 0; which < 2; ++which) {
         const S *src = (which ? v_src : k_src) + tok * kv_dim;
-        uint8_t *pool = which ? v_pool : k_pool;
-        float x[NC][8];
-        float mx = 0.f;
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
             const int c = lane + 64 * i;
             if (c < nchunks) {
-                load8(src + 8 * c, x[i]);
+                load8(src + 8 * c, xkv[which][i]);
             } else {
 #pragma unroll
-                for (int k = 0; k < 8; ++k) x[i][k] = 0.f;
+                for (int k = 0; k < 8; ++k) xkv[which][i][k] = 0.f;
             }
+        }
+    }
+#pragma unroll
+    for (int which = 0; which < 2; ++which) {
+        uint8_t *pool = which ? v_pool : k_pool;
+        float (&x)[NC][8] = xkv[which];
+        float mx = 0.f;
+#pragma unroll
+        for (int i = 0; i < NC; ++i)
 #pragma unroll
             for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(x[i][k]));
-        }
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
         const float scale = mx / qmax;
