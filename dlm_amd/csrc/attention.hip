@@ -887,15 +887,81 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Pass 2: log-sum-exp merge of a sequence's partitions.  One work-group per
-// (query row, sequence): the block reduces the partitions' max M, then wave w
-// accumulates partitions w, w + W, ... (every load independent, so many are
-// in flight), and the W partial sums meet in LDS.
+// Pass 2: log-sum-exp merge of a sequence's partitions.  Rows of up to
+// kCombineBatch partitions: one wave per (query row, sequence), kCombineWaves
+// rows per work-group.
 // ---------------------------------------------------------------------------
 constexpr int kCombineWaves = 4;
+constexpr int kCombineBatch = 8;
 
 template <int D>
-__global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_kernel(
+__global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wave_kernel(
+    void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
+    const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
+    int max_blocks, int partition, int max_parts) {
+    constexpr int DPL = D / 64;  // dims per lane
+    constexpr int B = kCombineBatch;  // partitions loaded per batch
+    // One wave per (sequence, query row), kCombineWaves rows per work-group:
+    // the wave folds all of the row's partitions itself (online rescale), so
+    // no cross-wave merge and a quarter of the work-groups of one per row.
+    const int seq = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kCombineWaves + (threadIdx.x >> 6);
+    if (r >= rows_per_seq) return;
+    const int64_t row = (int64_t)seq * rows_per_seq + r;
+    const float *ml = ws_ml + 2 * row * max_parts;
+    const float *o = ws_o + row * max_parts * D;
+
+    float mb[B], lb[B], ob[B][DPL];
+    auto load = [&](int p0, int last) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int p = min(p0 + i, last);
+            mb[i] = ml[2 * p];
+            lb[i] = ml[2 * p + 1];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) ob[i][k] = o[(int64_t)p * D + lane + 64 * k];
+        }
+    };
+    // The first batch is read before the context length is known (every
+    // slot below max_parts exists; only those below nparts are used), so
+    // rows of up to B partitions cost one memory round trip.
+    load(0, max_parts - 1);
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    const int nparts = parts_of(ctx, partition);
+    if (nparts == 1) return;
+
+    float m = -INFINITY, L = 0.f, O[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) O[k] = 0.f;
+    for (int p0 = 0;;) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            if (p0 + i >= nparts) break;
+            const float mn = fmaxf(m, mb[i]);
+            if (mn == -INFINITY) continue;  // both empty
+            const float fa = m == -INFINITY ? 0.f : exp2f(m - mn);
+            const float fb = mb[i] == -INFINITY ? 0.f : exp2f(mb[i] - mn);
+            L = fa * L + fb * lb[i];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) O[k] = fa * O[k] + fb * ob[i][k];
+            m = mn;
+        }
+        p0 += B;
+        if (p0 >= nparts) break;
+        load(p0, nparts - 1);
+    }
+#pragma unroll
+    for (int k = 0; k < DPL; ++k)
+        store_out(out, out_dtype, row * D + lane + 64 * k, L > 0.f ? O[k] / L : 0.f);
+}
+
+// Rows of more than kCombineBatch partitions: one work-group of
+// kCombineWaves waves per (query row, sequence).  Wave w loads its first
+// partition (w) before the context length arrives, folds w + W, ... in
+// batches with an online rescale, and the waves merge once in LDS.
+template <int D>
+__global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
     const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
     int max_blocks, int partition, int max_parts) {
@@ -1019,8 +1085,18 @@ int launch_pair(const Args &a, int partition, Launch launch) {
         ws_ml = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + a.ws_o_bytes);
     }
     launch(dim3((unsigned)(a.B * a.Hkv), (unsigned)max_parts), max_parts, ws_o, ws_ml);
-    if (max_parts > 1)
-        hipLaunchKernelGGL(paged_attn_combine_kernel<D>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
+    // Rows of up to kCombineBatch partitions: a wave per row (config 5
+    // 64.9 -> 66.2%); longer rows: a work-group per row, whose four waves
+    // share the row's partitions (the wave-per-row kernel was 0.8 points
+    // slower at config 4's 32 partitions and 2.9 us slower in the decode
+    // block's 32).
+    if (max_parts > kCombineBatch)
+        hipLaunchKernelGGL(paged_attn_combine_wg_kernel<D>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
+                           dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
+                           a.NQ * a.Hq, a.max_blocks, partition, max_parts);
+    else if (max_parts > 1)
+        hipLaunchKernelGGL(paged_attn_combine_wave_kernel<D>,
+                           dim3((unsigned)((a.NQ * a.Hq + kCombineWaves - 1) / kCombineWaves), (unsigned)a.B),
                            dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
                            a.NQ * a.Hq, a.max_blocks, partition, max_parts);
     hipError_t e = hipGetLastError();

@@ -122,6 +122,7 @@ EDGE_CTX = [0, 1, 2, 15, 16, 17, 255, 256, 257, 511, 513, 1000]
     (np.float32, 32, 8, 64, 1, list(range(37, 1537, 37))),  # 40 seqs: 256-token partitions
     (np.float16, 32, 8, 128, 1, EDGE_CTX),                  # config-2 shape
     (np.float16, 32, 8, 128, 1, [1023, 1024, 1025, 2048, 2049]),  # partition edges
+    (np.float16, 32, 8, 128, 1, [9000, 100, 8193]),          # > 8 partitions: work-group combine
     (np.float16, 64, 8, 128, 1, [4000, 17, 2049]),          # 70B shape, GQA 8
     (np.float16, 8, 8, 128, 1, [100, 700]),                 # MHA (group 1)
     (np.float16, 16, 8, 64, 1, [100, 700]),                 # group 2, d 64
