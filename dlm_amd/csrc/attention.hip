@@ -1122,10 +1122,15 @@ int launch_mfma(const Args &a) {
     });
 }
 
-// 256-token partitions, or one block per wave when that grid would not fill
-// the chip: a single decoding sequence (dlmk_decode_block_paged) has num_kv_heads
-// x ctx / 256 work-groups, 64 at the 8B shape and ctx 2048 on 256 compute units.
+// 256-token partitions when that grid fills the chip; otherwise smaller
+// partitions, as large as still give kValuMinGrid work-groups (a single
+// decoding sequence, as in dlmk_decode_block_paged, has num_kv_heads x
+// ctx / 256 work-groups: 64 at the 8B shape and ctx 2048).  Measured at the
+// decode block's shape (ctx 2048: 128 work-groups with 128-token partitions)
+// 128-token beat 64-token partitions by 1.1 us a layer; at config 1's
+// (ctx 640: 40 of them) 64-token ones won by 0.4 us.
 constexpr int64_t kValuSmallGrid = 1024;  // work-groups
+constexpr int64_t kValuMinGrid = 128;
 
 template <int D, int GQA, int NQ, int NW, int P>
 int launch_valu_p(const Args &a) {
@@ -1143,9 +1148,10 @@ int launch_valu_p(const Args &a) {
 template <int D, int GQA, int NQ>
 int launch_valu(const Args &a) {
     constexpr int NW = GQA * NQ <= 4 ? 4 : 8;
-    if ((int64_t)a.B * a.Hkv * parts_for(a.max_blocks, 256) < kValuSmallGrid)
-        return launch_valu_p<D, GQA, NQ, NW, NW * kBlock>(a);
-    return launch_valu_p<D, GQA, NQ, NW, 256>(a);
+    const auto grid = [&](int p) { return (int64_t)a.B * a.Hkv * parts_for(a.max_blocks, p); };
+    if (grid(256) >= kValuSmallGrid) return launch_valu_p<D, GQA, NQ, NW, 256>(a);
+    if (grid(128) >= kValuMinGrid) return launch_valu_p<D, GQA, NQ, NW, 128>(a);
+    return launch_valu_p<D, GQA, NQ, NW, NW * kBlock>(a);
 }
 
 int unsupported_rows(int gqa, int nq) {

@@ -117,8 +117,8 @@ EDGE_CTX = [0, 1, 2, 15, 16, 17, 255, 256, 257, 511, 513, 1000]
 
 
 @pytest.mark.parametrize("dtype,Hq,Hkv,d,nq,ctx", [
-    (np.float32, 32, 8, 64, 1, [576, 1, 300]),             # config-1 shape (Llama-3.2-1B)
-    (np.float32, 32, 8, 64, 1, EDGE_CTX),                   # small grid: 64-token partitions
+    (np.float32, 32, 8, 64, 1, [576, 1, 300]),             # config-1 shape: 64-token partitions
+    (np.float32, 32, 8, 64, 1, EDGE_CTX),                   # small grid: 128-token partitions
     (np.float32, 32, 8, 64, 1, list(range(37, 1537, 37))),  # 40 seqs: 256-token partitions
     (np.float16, 32, 8, 128, 1, EDGE_CTX),                  # config-2 shape
     (np.float16, 32, 8, 128, 1, [1023, 1024, 1025, 2048, 2049]),  # partition edges
