@@ -86,11 +86,11 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 // round(x / scale) clamped to +-127 (+-7) -- NaN quotients give code 0, as
 // Rust's saturating `as i8` does -- and an all-zero vector scale 0.
 //
-// One wavefront per token.  Lane l owns the 8-dim chunks l, l + 64, ... of
-// the token (NC of them, kept in registers): one 16-byte source load per chunk
-// (two for f32), a wave max-reduction, then the stores into the tiles the
-// attention kernel reads 16 bytes a lane at a time (head_dim a multiple of
-// 64; KG, VG as below):
+// One work-group per token: threads 0..127 own K's 8-dim chunks t, t + 128,
+// ... (kept in registers), threads 128..255 V's: one 16-byte source load per
+// chunk (two for f32), a max-reduction over the pool's two waves, then the
+// stores into the tiles the attention kernel reads 16 bytes a lane at a time
+// (head_dim a multiple of 64; KG, VG as below):
 //   K [d/KG][16 tokens][KG dims], KG = 16 (int8) or 32 / 16 (int4, d % 128
 //     == 0 or not): a chunk is one 8-byte (int8) or 4-byte (int4) store;
 //   V [d/(16 VG)][4 token quads][16][VG dims][4 tokens], VG = 4 (int8) or
@@ -129,9 +129,12 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
     const int64_t *__restrict__ slots, int64_t n_tok, int num_kv_heads, int head_dim,
     int64_t num_slots) {
     constexpr int BS = 16;
-    const int64_t tok = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-    const int lane = threadIdx.x & 63;
-    if (tok >= n_tok) return;
+    // One work-group per token: threads 0..127 quantize K, 128..255 V, each
+    // over chunks lt, lt + 128, ... (NC of them); a pool's max meets across
+    // its two waves in LDS.
+    __shared__ float red[4];
+    const int64_t tok = blockIdx.x;
+    const int lane = threadIdx.x & 63, which = threadIdx.x >> 7, lt = threadIdx.x & 127;
     const int64_t slot = slots[tok];
     if (slot < 0 || slot >= num_slots) return;
     const int64_t blk = slot / BS;
@@ -144,41 +147,34 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
     const int KG = QBITS == 8 ? 16 : (d % 128 == 0 ? 32 : 16);
     const int VG = QBITS == 8 ? 4 : (d % 128 == 0 ? 8 : 4);
     const int VLANE = VG * QBITS / 2;
-    // K's and V's source chunks are loaded together, before any pool store
-    // (the stores could alias the sources as far as the compiler knows, so
-    // V's loads would otherwise wait for K's stores).
-    float xkv[2][NC][8];
-#pragma unroll
-    for (int which = 0; which < 2; ++which) {
+    {
         const S *src = (which ? v_src : k_src) + tok * kv_dim;
-#pragma unroll
-        for (int i = 0; i < NC; ++i) {
-            const int c = lane + 64 * i;
-            if (c < nchunks) {
-                load8(src + 8 * c, xkv[which][i]);
-            } else {
-#pragma unroll
-                for (int k = 0; k < 8; ++k) xkv[which][i][k] = 0.f;
-            }
-        }
-    }
-#pragma unroll
-    for (int which = 0; which < 2; ++which) {
         uint8_t *pool = which ? v_pool : k_pool;
-        float (&x)[NC][8] = xkv[which];
+        float x[NC][8];
         float mx = 0.f;
 #pragma unroll
-        for (int i = 0; i < NC; ++i)
+        for (int i = 0; i < NC; ++i) {
+            const int c = lt + 128 * i;
+            if (c < nchunks) {
+                load8(src + 8 * c, x[i]);
+            } else {
+#pragma unroll
+                for (int k = 0; k < 8; ++k) x[i][k] = 0.f;
+            }
 #pragma unroll
             for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(x[i][k]));
+        }
 #pragma unroll
         for (int o = 1; o < 64; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+        if (lane == 0) red[threadIdx.x >> 6] = mx;
+        __syncthreads();
+        mx = fmaxf(red[2 * which], red[2 * which + 1]);
         const float scale = mx / qmax;
         const float ok = scale > 0.f ? 1.f : 0.f;
-        if (lane == 0) (which ? v_scales : k_scales)[slot] = ok != 0.f ? scale : 0.f;
+        if (lt == 0) (which ? v_scales : k_scales)[slot] = ok != 0.f ? scale : 0.f;
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
-            const int c = lane + 64 * i;
+            const int c = lt + 128 * i;
             if (c >= nchunks) continue;
             const int h = (8 * c) / d, j = 8 * c - h * d;
             uint8_t *tile = pool + (blk * num_kv_heads + h) * tile_bytes;
@@ -294,16 +290,15 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
                           "dlmk_kv_append_quant: head_dim %d (multiple of 64) / block_size %d (16)",
                           head_dim, block_size);
     const int64_t kv_dim = (int64_t)num_kv_heads * head_dim;
-    const int64_t chunks_per_lane = dlmk::ceil_div(kv_dim / 8, 64);
-    if (chunks_per_lane > 16)
+    const int64_t chunks_per_lane = dlmk::ceil_div(kv_dim / 8, 128);
+    if (chunks_per_lane > 8)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED,
                           "dlmk_kv_append_quant: kv_dim %lld above 8192", (long long)kv_dim);
     if (reinterpret_cast<uintptr_t>(k_src) % 16 || reinterpret_cast<uintptr_t>(v_src) % 16)
         return dlmk::fail(DLMK_ERR_INVALID_ARG,
                           "dlmk_kv_append_quant: k_src / v_src not 16-byte aligned");
-    const int nc = chunks_per_lane <= 1 ? 1 : chunks_per_lane <= 2 ? 2 : chunks_per_lane <= 4 ? 4
-                 : chunks_per_lane <= 8 ? 8 : 16;
-    const int64_t gx = dlmk::ceil_div(n_tok, 4);
+    const int nc = chunks_per_lane <= 1 ? 1 : chunks_per_lane <= 2 ? 2 : chunks_per_lane <= 4 ? 4 : 8;
+    const int64_t gx = n_tok;
     if (gx > 0x7fffffff) return dlmk::fail(DLMK_ERR_UNSUPPORTED, "dlmk_kv_append_quant: grid too large");
     auto s = (hipStream_t)stream;
     const int64_t num_slots = num_blocks * block_size;
@@ -317,8 +312,7 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
         case 1: DLMK_LAUNCH_NC(Q, S, 1); break;                       \
         case 2: DLMK_LAUNCH_NC(Q, S, 2); break;                       \
         case 4: DLMK_LAUNCH_NC(Q, S, 4); break;                       \
-        case 8: DLMK_LAUNCH_NC(Q, S, 8); break;                       \
-        default: DLMK_LAUNCH_NC(Q, S, 16); break;                     \
+        default: DLMK_LAUNCH_NC(Q, S, 8); break;                      \
     }
     const int q = quant == DLMK_I8 ? 8 : 4;
     switch (src_dtype * 16 + q) {
