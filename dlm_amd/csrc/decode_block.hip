@@ -16,10 +16,10 @@
 //                        of resident work-groups; RW output rows per wave,
 //                        16-byte weight loads, 16 in flight per lane (8 per
 //                        matrix for SwiGLU) plus the next step's prefetched,
-//                        wave reduction; epilogue = bias store, residual add,
-//                        or (two matrices) SwiGLU; q, k and v as one launch.
-//                        The q/k/v launch's epilogue is RoPE (NeoX split-half,
-//                        host-computed inv_freq) over row pairs of one head,
+//                        wave reduction; epilogue = residual add, (two
+//                        matrices) SwiGLU, or, for q, k and v as one launch,
+//                        biases and RoPE (NeoX split-half, host-computed
+//                        inv_freq) over row pairs of one head,
 //                        with the new token's K and V written straight into
 //                        the pools at the slot the block table gives; it also
 //                        writes the context length the attention reads.
@@ -171,14 +171,14 @@ __host__ __device__ inline QOffsets qoffsets(int dt, int64_t n, int64_t gs) {
     return QOffsets{s, s + groups * 4};
 }
 
-enum Epilogue { kStoreBias = 0, kAddInto = 1, kSwiGLU = 2, kRopeAppend = 3 };
+enum Epilogue { kAddInto = 1, kSwiGLU = 2, kRopeAppend = 3 };
 
 // Up to three matrices over the same input, as one launch (q, k and v share
 // the normalised hidden state).  A segment's rows follow the previous
 // segment's in the launch's row numbering.
 struct GemvSeg {
     const uint8_t *W, *W2;  // W2: the up projection of the SwiGLU epilogue
-    const float *bias;      // kStoreBias: may be null
+    const float *bias;      // kRopeAppend: may be null
     float *out;
     int rows;
 };
@@ -210,9 +210,9 @@ struct GemvArgs {
 // launch rows (b * kGemvWaves + w) * RW + k * gridDim.x * kGemvWaves * RW,
 // RW rows at a time, so a grid of resident work-groups amortises the staging
 // over several rows and each x read over RW rows: 16-byte weight loads, U in
-// flight per lane per row, a wave reduction per row.  Epilogues: kStoreBias
-// out[o] = dot (+ bias[o]); kAddInto out[o] += dot (the residual); kSwiGLU
-// out[o] = silu(dot(W)) * dot(W2).
+// flight per lane per row, a wave reduction per row.  Epilogues: kAddInto
+// out[o] += dot (the residual); kSwiGLU out[o] = silu(dot(W)) * dot(W2);
+// kRopeAppend (q, k, v + biases, then RoPE and the paged append).
 //
 // Measured on the 8B layer (bf16): the x reads from LDS, not the weight
 // stream, bounded these kernels -- down_proj took 34.9 us with the dot
@@ -464,9 +464,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
                 const float s1 = wave_sum<64>(acc[j]);
                 const float s2 = kTwo ? wave_sum<64>(acc2[j]) : 0.f;
                 if (lane == 0 && r0 + j < a.total_rows) {
-                    if constexpr (EPI == kStoreBias) {
-                        Rc.g[j].out[Rc.o[j]] = s1 + (Rc.g[j].bias ? Rc.g[j].bias[Rc.o[j]] : 0.f);
-                    } else if constexpr (EPI == kAddInto) {
+                    if constexpr (EPI == kAddInto) {
                         Rc.g[j].out[Rc.o[j]] = Rc.g[j].out[Rc.o[j]] + s1;
                     } else {
                         // silu(gate) * up, cpu.rs:960-975
@@ -550,9 +548,7 @@ void launch_gemv_epi(hipStream_t st, const GemvArgs &a) {
 
 template <int DT>
 void launch_gemv(int epi, hipStream_t st, const GemvArgs &a) {
-    if (epi == kStoreBias)
-        launch_gemv_epi<DT, kStoreBias>(st, a);
-    else if (epi == kAddInto)
+    if (epi == kAddInto)
         launch_gemv_epi<DT, kAddInto>(st, a);
     else if (epi == kSwiGLU)
         launch_gemv_epi<DT, kSwiGLU>(st, a);
