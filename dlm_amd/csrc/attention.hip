@@ -28,6 +28,8 @@
 //     IS the A-operand layout of this product, so P never leaves registers;
 //     the B operand is 4 tokens x 1 dim = 8 contiguous bytes of the V tile
 //     [d][16].
+// int8 / int4 pools: the same kernel over f16 operands widened in registers
+//   from tiles laid out for 16-byte loads per lane (storage codecs below).
 // f32 pools: VALU kernel (dot products with FMA, cross-lane sums).
 
 #include <hip/hip_runtime.h>
@@ -55,17 +57,18 @@ constexpr float kLog2e = 1.4426950408889634f;
 #ifndef DLMK_MFMA_PD
 #define DLMK_MFMA_PD 2
 #endif
-// Prefetch depth for int8 / int4 pools, whose tiles are 2x / 4x smaller.
 // Minimum waves per SIMD for the quantized-pool kernels: half the bytes per
 // tile leave the per-tile latency chain exposed, so they trade registers for
 // occupancy.
 #ifndef DLMK_MFMA_QWAVES
 #define DLMK_MFMA_QWAVES 3
 #endif
+// Prefetch depth for int8 / int4 pools, whose tiles are 2x / 4x smaller.
 #ifndef DLMK_MFMA_PDQ
 #define DLMK_MFMA_PDQ 2
 #endif
-// Minimum waves per SIMD the register allocation must allow (0: compiler's choice).
+// Minimum waves per SIMD the register allocation must allow for every pool
+// format (0: per-format defaults above; a tuning override).
 #ifndef DLMK_MFMA_WPE
 #define DLMK_MFMA_WPE 0
 #endif
