@@ -241,6 +241,34 @@ def test_paged_attention_workspace_reuse_across_shapes(oracle, torch_mod, ops, c
                          f"rep {rep} B={len(w.ctx)} Hq={w.Hq} nq={w.nq}")
 
 
+@pytest.mark.parametrize("dtype,ctx,table_blocks", [
+    (np.float16, [100, 1500, 3000], 256),      # <= 8 partitions a row: wave-per-row combine
+    (np.float16, [100, 1500, 9000], 600),      # > 8: work-group-per-row combine
+    (np.float32, [40, 700, 1000], 64),         # f32, 128-token partitions
+])
+def test_paged_attention_nan_workspace(oracle, torch_mod, ops, cuda, dtype, ctx, table_blocks):
+    """The combine kernels read workspace slots past a row's partition count
+    before they know it: a workspace full of NaN there changes nothing."""
+    torch = torch_mod
+    banner(f"attention NaN workspace dtype={np.dtype(dtype).name} ctx={ctx}")
+    rng = np.random.default_rng(41 + len(ctx) + table_blocks)
+    w = make_workload(rng, ctx, 32, 8, 64 if dtype is np.float32 else 128, dtype,
+                      sigma=1.0 if dtype is np.float32 else 0.5)
+    tables = np.zeros((len(ctx), table_blocks), np.int32)
+    tables[:, :w.tables.shape[1]] = w.tables
+    w.tables = tables  # wider tables: more partition slots than any row uses
+    need = ops.attention_workspace_bytes(len(w.ctx), w.nq, w.Hq, w.d, table_blocks)
+    ws = ops.alloc_workspace(need, cuda)
+    ws.fill_(255)  # every f32 in it is a NaN
+    out = ops.paged_decode_attention(
+        to_dev(torch, w.q, cuda), to_dev(torch, w.k_pool, cuda), to_dev(torch, w.v_pool, cuda),
+        to_dev(torch, w.tables, cuda), to_dev(torch, w.ctx, cuda), num_kv_heads=w.Hkv,
+        scale=float(w.scale), out_dtype=torch.float32, workspace=ws)
+    torch.cuda.synchronize()
+    atol, rtol = (F32_ATOL, F32_RTOL) if dtype is np.float32 else (F16_ATOL, F16_RTOL)
+    assert_close(out.cpu().numpy(), oracle_attention(oracle, w), atol, rtol, "NaN workspace")
+
+
 def test_paged_attention_unsupported_shape_raises(torch_mod, ops, cuda):
     torch = torch_mod
     from dlm_amd import DlmkError
