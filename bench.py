@@ -287,9 +287,12 @@ def copy_calibration(torch, ops, steps):
                                            "bytes_written_per_launch": 2 * 4096 * bb}}))
 
 
-def cpu_baseline(w, budget_s):
+def cpu_baseline(w, budget_s, max_threads=16):
     """dlm's CPU attention path (the oracle restatement, 1 thread) on a bounded
-    sample of the same workload: as many sequences as fit budget_s."""
+    sample of the same workload: as many sequences as fit budget_s.  The same
+    sample is then run again over up to max_threads host threads, one sequence
+    each at a time (an extension: dlm steps sessions serially), reported
+    beside the 1-thread figure."""
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
     from oracle import oracle as orc
     orc.build()
@@ -298,6 +301,7 @@ def cpu_baseline(w, budget_s):
     X = 16 // np.dtype(npdt).itemsize
     done_tok, done_seq, elapsed, nbytes = 0, 0, 0.0, 0
     qcode = {"int8": orc.I8, "int4": orc.I4}.get(w.quant)
+    jobs = []  # the sample's calls, replayed over threads below
     while elapsed < budget_s and done_seq < 4096:
         c = int(rng.integers(w.ctx[0], w.ctx[1] + 1))
         nb = -(-c // BS)
@@ -306,23 +310,38 @@ def cpu_baseline(w, budget_s):
         if qcode is None:
             kp = (rng.standard_normal((nb, w.hkv, w.d // X, BS, X)) * 0.5).astype(npdt)
             vp = (rng.standard_normal((nb, w.hkv, w.d, BS)) * 0.5).astype(npdt)
+            job = (lambda q=q, kp=kp, vp=vp, table=table, c=c:
+                   orc.paged_attention(q, kp, vp, table, np.array([c], np.int32), w.nq, w.hq,
+                                       w.hkv, w.d, BS, 1.0 / np.sqrt(w.d)))
             t0 = time.perf_counter()
-            orc.paged_attention(q, kp, vp, table, np.array([c], np.int32), w.nq, w.hq, w.hkv, w.d,
-                                BS, 1.0 / np.sqrt(w.d))
+            job()
         else:
             ks, vs = orc.quant_pool_shapes(nb, w.hkv, w.d, qcode)
             kp = rng.integers(0, 256, ks, dtype=np.uint8)
             vp = rng.integers(0, 256, vs, dtype=np.uint8)
             ksc = rng.random((nb, BS), dtype=np.float32) * 0.02
             vsc = rng.random((nb, BS), dtype=np.float32) * 0.02
+            qf = q.astype(np.float32)
+            job = (lambda qf=qf, kp=kp, vp=vp, ksc=ksc, vsc=vsc, table=table, c=c:
+                   orc.paged_attention_quant(qf, kp, vp, ksc, vsc, qcode, table,
+                                             np.array([c], np.int32), w.nq, w.hq, w.hkv, w.d,
+                                             1.0 / np.sqrt(w.d)))
             t0 = time.perf_counter()
-            orc.paged_attention_quant(q.astype(np.float32), kp, vp, ksc, vsc, qcode, table,
-                                      np.array([c], np.int32), w.nq, w.hq, w.hkv, w.d,
-                                      1.0 / np.sqrt(w.d))
+            job()
         elapsed += time.perf_counter() - t0
+        jobs.append(job)
         done_tok += c
         done_seq += 1
         nbytes += attn_bytes(w, [c], elem_bytes(w))
+    # The same calls over threads (the C oracle releases the GIL in ctypes
+    # calls and keeps no shared state).
+    from concurrent.futures import ThreadPoolExecutor
+    threads = max(1, min(max_threads, os.cpu_count() or 1))
+    t0 = time.perf_counter()
+    with ThreadPoolExecutor(max_workers=threads) as ex:
+        list(ex.map(lambda f: f(), jobs))
+    par_s = time.perf_counter() - t0
+    del jobs
     return {
         "value": round(nbytes / elapsed / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
         "sample": (f"oracle/oracle.c paged attention{'' if qcode is None else ' over ' + w.quant + ' pools'} "
@@ -331,6 +350,10 @@ def cpu_baseline(w, budget_s):
                    f"{elapsed:.1f} s; same algorithmic-bytes formula"),
         "context_tokens_per_s": round(done_tok / elapsed, 1),
         "cpu_model": _cpu_model(), "host_nproc": os.cpu_count(),
+        "extension_threads": {"threads": threads, "value": round(nbytes / par_s / 1e9, 4),
+                              "unit": "GB/s", "seconds": round(par_s, 2),
+                              "note": "same sample, one sequence per thread at a time; "
+                                      "dlm itself steps sessions serially"},
     }
 
 
