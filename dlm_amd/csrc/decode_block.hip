@@ -40,7 +40,6 @@ constexpr int kBlock = 16;  // tokens per KV block
 #define DLMK_GEMV_WAVES 4
 #endif
 constexpr int kGemvWaves = DLMK_GEMV_WAVES;
-constexpr int kGemvUnroll = 8;  // 16-byte weight loads in flight per lane
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 

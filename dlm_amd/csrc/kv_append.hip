@@ -135,6 +135,7 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
     __shared__ float red[4];
     const int64_t tok = blockIdx.x;
     const int lane = threadIdx.x & 63, which = threadIdx.x >> 7, lt = threadIdx.x & 127;
+    if (tok >= n_tok) return;  // the grid is n_tok work-groups; uniform per work-group
     const int64_t slot = slots[tok];
     if (slot < 0 || slot >= num_slots) return;
     const int64_t blk = slot / BS;
