@@ -4,9 +4,11 @@
 // slot `num_positions` of a flat f32 buffer (src/gpu/kernels.cu:267-270 used at
 // :361-363) -- with one launch that scatters every token of a decode step or a
 // prefill chunk into its physical block through a slot mapping.  It is a pure
-// bit copy, so f32, f16 and bf16 share one kernel keyed on element size.
+// bit copy, so f32, f16 and bf16 share the kernels, keyed on element size.
+// Appends of 512 tokens or more in 16-token blocks use kv_append_run_kernel
+// (below); the rest use kv_append_kernel.
 //
-// Thread mapping: one thread moves CPT 16-byte chunks (X = 16 / elem_bytes
+// kv_append_kernel thread mapping: one thread moves CPT 16-byte chunks (X = 16 / elem_bytes
 // consecutive dims each) of one (token, kv head).  Tokens are the fastest-varying
 // index inside a wavefront, so lanes holding consecutive tokens of the same
 // block write one contiguous run of K chunks ([d/X][bs][X] rows) and, per dim,
@@ -69,6 +71,70 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(
         E *vrow = reinterpret_cast<E *>(v_pool + tile) + (int64_t)chunk * X * block_size + t;
 #pragma unroll
         for (int e = 0; e < X; ++e) vrow[(int64_t)e * block_size] = ve[e];
+    }
+}
+
+// Prefill-sized appends (block size 16): one work-group per run of 16
+// consecutive source tokens and one kv head, 16 * cpl threads (cpl = 16-byte
+// chunks per head row; thread i holds chunk i % cpl of token i / cpl), so each
+// token's head row is read by cpl consecutive lanes.  When the run's slots
+// fill one block in order -- every full block of a prefill chunk -- the K and
+// V tiles are transposed in LDS and written as one contiguous run of 16-byte
+// stores; otherwise each thread stores its own chunk as kv_append_kernel does.
+// LDS rows are padded by one 16-byte unit per chunk to spread the banks.
+constexpr int kRunTokens = 16;
+constexpr int kRunMaxThreads = 1024;
+constexpr int64_t kRunMinTokens = 512;
+
+template <int EB>
+__global__ __launch_bounds__(kRunMaxThreads) void kv_append_run_kernel(
+    char *__restrict__ k_pool, char *__restrict__ v_pool, const char *__restrict__ k_src,
+    const char *__restrict__ v_src, const int64_t *__restrict__ slots, int64_t n_tok,
+    int num_kv_heads, int head_dim, int64_t num_slots) {
+    using E = typename Bits<EB>::type;
+    constexpr int X = 16 / EB, BS = kRunTokens, PAD = BS + 1;
+    __shared__ uint4 k_lds[kRunMaxThreads / BS * PAD];
+    __shared__ uint4 v_lds[kRunMaxThreads / BS * PAD];
+    const int cpl = head_dim / X;
+    const int i = threadIdx.x, t = i / cpl, chunk = i - t * cpl;
+    const int head = blockIdx.y;
+    const int64_t tok0 = (int64_t)blockIdx.x * BS, tok = tok0 + t;
+    const bool have = tok < n_tok;
+    int64_t slot = -1;
+    uint4 kc = {0, 0, 0, 0}, vc = {0, 0, 0, 0};
+    if (have) {
+        slot = slots[tok];
+        const int64_t off = ((tok * num_kv_heads + head) * head_dim) * EB + (int64_t)chunk * 16;
+        kc = *reinterpret_cast<const uint4 *>(k_src + off);
+        vc = *reinterpret_cast<const uint4 *>(v_src + off);
+    }
+    const int64_t slot0 = slots[tok0];  // tok0 < n_tok: the grid is ceil(n_tok / 16) runs
+    const bool in_run = have && slot0 >= 0 && slot0 % BS == 0 && slot0 + BS <= num_slots && slot == slot0 + t;
+    if (__syncthreads_and(in_run)) {
+        // K tile [cpl][16][X]: this chunk is unit chunk * 16 + t.  V tile
+        // [d][16]: element (chunk * X + e, t); 16-byte unit u of the tile is
+        // chunk u / 16 of it.
+        k_lds[chunk * PAD + t] = kc;
+        E ve[X];
+        __builtin_memcpy(ve, &vc, 16);
+        E *vrow = reinterpret_cast<E *>(v_lds + chunk * PAD);
+#pragma unroll
+        for (int e = 0; e < X; ++e) vrow[e * BS + t] = ve[e];
+        __syncthreads();
+        const int64_t tile = ((slot0 / BS) * num_kv_heads + head) * (int64_t)head_dim * BS * EB;
+        const int u = (i / BS) * PAD + i % BS;
+        reinterpret_cast<uint4 *>(k_pool + tile)[i] = k_lds[u];
+        reinterpret_cast<uint4 *>(v_pool + tile)[i] = v_lds[u];
+    } else if (have && slot >= 0 && slot < num_slots) {
+        const int64_t blk = slot / BS;
+        const int tt = (int)(slot - blk * BS);
+        const int64_t tile = ((blk * num_kv_heads + head) * (int64_t)head_dim * BS) * EB;
+        *reinterpret_cast<uint4 *>(k_pool + tile + ((int64_t)chunk * BS + tt) * 16) = kc;
+        E ve[X];
+        __builtin_memcpy(ve, &vc, 16);
+        E *vrow = reinterpret_cast<E *>(v_pool + tile) + (int64_t)chunk * X * BS + tt;
+#pragma unroll
+        for (int e = 0; e < X; ++e) vrow[(int64_t)e * BS] = ve[e];
     }
 }
 
@@ -241,18 +307,38 @@ extern "C" int dlmk_kv_append(void *stream, void *k_pool, void *v_pool, const vo
         return dlmk::fail(DLMK_ERR_UNSUPPORTED, "dlmk_kv_append: head_dim*elem_bytes (%d) not a multiple of 16",
                           head_dim * eb);
     const int cpl = head_dim * eb / 16;
-    // Two chunks per thread for prefill-sized appends where the head row
-    // allows (config 3's 2096 tokens 13.4 -> 9.5 us, a 16384-token prefill
-    // 4.8 -> 5.1 TB/s); one for decode-sized ones (64 tokens: 2.70 us against
-    // 3.11 with two).
+    auto s = (hipStream_t)stream;
+    const int64_t num_slots = num_blocks * block_size;
+    // Prefill-sized appends in 16-token blocks: runs of 16 tokens per
+    // work-group (coalesced source rows, whole-tile stores for full blocks;
+    // 2096 tokens 9.6 -> 5.7 us, a 16384-token prefill 5.55 -> 6.38 TB/s).
+    if (n_tok >= kRunMinTokens && block_size == kRunTokens && cpl * kRunTokens <= kRunMaxThreads) {
+        const int64_t rx = dlmk::ceil_div(n_tok, (int64_t)kRunTokens);
+        if (rx > 0x7fffffff || num_kv_heads > 65535)
+            return dlmk::fail(DLMK_ERR_UNSUPPORTED, "dlmk_kv_append: grid too large");
+        dim3 rgrid((unsigned)rx, (unsigned)num_kv_heads);
+        if (eb == 2)
+            hipLaunchKernelGGL(kv_append_run_kernel<2>, rgrid, dim3(cpl * kRunTokens), 0, s, (char *)k_pool,
+                               (char *)v_pool, (const char *)k_src, (const char *)v_src, slot_mapping, n_tok,
+                               num_kv_heads, head_dim, num_slots);
+        else
+            hipLaunchKernelGGL(kv_append_run_kernel<4>, rgrid, dim3(cpl * kRunTokens), 0, s, (char *)k_pool,
+                               (char *)v_pool, (const char *)k_src, (const char *)v_src, slot_mapping, n_tok,
+                               num_kv_heads, head_dim, num_slots);
+        hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return dlmk::fail((int)e, "dlmk_kv_append launch: %s", hipGetErrorString(e));
+        return DLMK_OK;
+    }
+    // Outside the run kernel's range: two chunks per thread for appends of
+    // 512 tokens or more where the head row allows (a 2096-token append 13.4
+    // -> 9.5 us in 16-token blocks), one for decode-sized ones (64 tokens:
+    // 2.70 us against 3.11 with two).
     const int cpt = cpl % 2 == 0 && n_tok >= 512 ? 2 : 1;
     const int64_t gy = (int64_t)num_kv_heads * cpl / cpt;
     const int64_t gx = dlmk::ceil_div(n_tok, kThreads);
     if (gy > 65535 || gx > 0x7fffffff)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED, "dlmk_kv_append: grid too large");
     dim3 grid((unsigned)gx, (unsigned)gy);
-    auto s = (hipStream_t)stream;
-    const int64_t num_slots = num_blocks * block_size;
 #define DLMK_APPEND_LAUNCH(EB, CPT)                                                               \
     hipLaunchKernelGGL((kv_append_kernel<EB, CPT>), grid, dim3(kThreads), 0, s, (char *)k_pool,    \
                        (char *)v_pool, (const char *)k_src, (const char *)v_src, slot_mapping, n_tok, \

@@ -36,12 +36,19 @@ def ops(cuda):
     (np.float16, 2, 64, 300, True),
     (np.float16, 2, 24, 50, True),    # 3 chunks per head row: one chunk per thread
     ("bf16", 8, 128, 100, False),
+    # >= 512 tokens: 16-token runs per work-group (whole-tile stores for full
+    # blocks, per-chunk stores otherwise) at 128 to 1024 threads
+    (np.float32, 8, 64, 640, True),
+    (np.float32, 1, 256, 520, "shifted"),  # runs straddle blocks
+    (np.float16, 4, 256, 700, True),
+    (np.float16, 2, 64, 600, False),     # no run fills a block
+    ("bf16", 8, 128, 1024, "shifted"),
 ])
 def test_kv_append_bit_exact(oracle, torch_mod, ops, cuda, dtype, Hkv, d, ntok, chunked):
     torch = torch_mod
     banner(f"kv_append dtype={dtype} Hkv={Hkv} d={d} ntok={ntok}")
     rng = np.random.default_rng(100 + ntok)
-    bs, nb = 16, ntok // 4 + 200
+    bs, nb = 16, ntok // 4 + 200 if chunked else max(ntok // 4 + 200, ntok + 64)
     npdt = np.float16 if dtype == "bf16" else dtype
     X = 16 // np.dtype(npdt).itemsize
     kp = rng.integers(0, 2**16, (nb, Hkv, d // X, bs, X)).astype(np.uint16) if npdt == np.float16 \
@@ -54,7 +61,8 @@ def test_kv_append_bit_exact(oracle, torch_mod, ops, cuda, dtype, Hkv, d, ntok, 
     vs = rng.standard_normal((ntok, Hkv, d)).astype(npdt)
     if chunked:  # runs of consecutive slots inside shuffled blocks
         blocks = rng.permutation(nb)
-        slots = np.array([blocks[p // bs] * bs + p % bs for p in range(ntok)], np.int64)
+        o = 5 if chunked == "shifted" else 0  # the chunk starts mid-block
+        slots = np.array([blocks[(p + o) // bs] * bs + (p + o) % bs for p in range(ntok)], np.int64)
     else:  # one token per sequence, each in its own block at a random offset
         slots = rng.permutation(nb)[:ntok].astype(np.int64) * bs + rng.integers(0, bs, ntok)
     slots[::37] = -1  # skipped tokens
