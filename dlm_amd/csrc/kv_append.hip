@@ -188,6 +188,50 @@ __device__ __forceinline__ int quant_code(float x, float inv_ok, float scale, fl
     return (inv_ok == 0.f || r != r) ? 0 : (int)fminf(fmaxf(r, -qmax), qmax);
 }
 
+// Stores the 8 offset-binary codes q of dims j .. j + 7 of token t into the
+// (block, kv head) tile at `tile` (K if which == 0, else V), in the layouts
+// described above.
+template <int QBITS>
+__device__ __forceinline__ void place_chunk(uint8_t *tile, int which, int j, int t, int d,
+                                            const int (&q)[8]) {
+    constexpr int BS = 16;
+    const int KG = QBITS == 8 ? 16 : (d % 128 == 0 ? 32 : 16);
+    const int VG = QBITS == 8 ? 4 : (d % 128 == 0 ? 8 : 4);
+    const int VLANE = VG * QBITS / 2;
+    // V: dim jj of this token sits at lane group (jj / VG) % 16 of
+    // quarter jj / (16 VG), word (jj % VG) / (dims per byte), byte t % 4.
+    const int vq = j / (16 * VG), vn = (j % (16 * VG)) / VG, vk = j % VG;
+    uint8_t *vbase = tile + ((int64_t)(vq * 4 + t / 4) * 16 + vn) * VLANE + t % 4;
+    if constexpr (QBITS == 8) {
+        if (which == 0) {
+            u32x2 w;
+            w[0] = (q[0] & 0xff) | (q[1] & 0xff) << 8 | (q[2] & 0xff) << 16 | (uint32_t)(q[3] & 0xff) << 24;
+            w[1] = (q[4] & 0xff) | (q[5] & 0xff) << 8 | (q[6] & 0xff) << 16 | (uint32_t)(q[7] & 0xff) << 24;
+            *reinterpret_cast<u32x2 *>(tile + ((j / KG) * BS + t) * KG + j % KG) = w;
+        } else {
+            // 8 dims = two lane groups of VG = 4 (vk == 0).
+#pragma unroll
+            for (int k = 0; k < 8; ++k) vbase[(k / 4) * VLANE + (k % 4) * 4] = (uint8_t)q[k];
+        }
+    } else {
+        uint8_t by[4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) by[m] = (uint8_t)((q[2 * m] & 0x0f) | (q[2 * m + 1] & 0x0f) << 4);
+        if (which == 0) {
+            uint32_t w = by[0] | by[1] << 8 | by[2] << 16 | (uint32_t)by[3] << 24;
+            *reinterpret_cast<uint32_t *>(tile + ((j / KG) * BS + t) * (KG / 2) + (j % KG) / 2) = w;
+        } else {
+            // Dim pair m of the chunk: VG = 8 keeps the chunk in one lane
+            // group (words vk/2 .. +3); VG = 4 spans two (vk == 0).
+#pragma unroll
+            for (int m = 0; m < 4; ++m) {
+                const int jj = vk + 2 * m;
+                vbase[(jj / VG) * VLANE + ((jj % VG) / 2) * 4] = by[m];
+            }
+        }
+    }
+}
+
 template <int QBITS, typename S, int NC>
 __global__ __launch_bounds__(256) void kv_append_quant_kernel(
     uint8_t *__restrict__ k_pool, uint8_t *__restrict__ v_pool, float *__restrict__ k_scales,
@@ -209,11 +253,6 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
     const int d = head_dim, kv_dim = num_kv_heads * head_dim, nchunks = kv_dim / 8;
     const float qmax = QBITS == 8 ? 127.f : 7.f;
     const int64_t tile_bytes = (int64_t)d * BS * QBITS / 8;
-    // Tile geometry (see above): KG dims per K chunk, VG dims per V lane
-    // group, VLANE bytes per V lane group.
-    const int KG = QBITS == 8 ? 16 : (d % 128 == 0 ? 32 : 16);
-    const int VG = QBITS == 8 ? 4 : (d % 128 == 0 ? 8 : 4);
-    const int VLANE = VG * QBITS / 2;
     {
         const S *src = (which ? v_src : k_src) + tok * kv_dim;
         uint8_t *pool = which ? v_pool : k_pool;
@@ -249,39 +288,7 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
 #pragma unroll
             // Offset binary in the pools: code c is stored as c + 128 (c + 8).
             for (int k = 0; k < 8; ++k) q[k] = quant_code(x[i][k], ok, scale, qmax) + (QBITS == 8 ? 128 : 8);
-            // V: dim jj of this token sits at lane group (jj / VG) % 16 of
-            // quarter jj / (16 VG), word (jj % VG) / (dims per byte), byte t % 4.
-            const int vq = j / (16 * VG), vn = (j % (16 * VG)) / VG, vk = j % VG;
-            uint8_t *vbase = tile + ((int64_t)(vq * 4 + t / 4) * 16 + vn) * VLANE + t % 4;
-            if constexpr (QBITS == 8) {
-                if (which == 0) {
-                    u32x2 w;
-                    w[0] = (q[0] & 0xff) | (q[1] & 0xff) << 8 | (q[2] & 0xff) << 16 | (uint32_t)(q[3] & 0xff) << 24;
-                    w[1] = (q[4] & 0xff) | (q[5] & 0xff) << 8 | (q[6] & 0xff) << 16 | (uint32_t)(q[7] & 0xff) << 24;
-                    *reinterpret_cast<u32x2 *>(tile + ((j / KG) * BS + t) * KG + j % KG) = w;
-                } else {
-                    // 8 dims = two lane groups of VG = 4 (vk == 0).
-#pragma unroll
-                    for (int k = 0; k < 8; ++k) vbase[(k / 4) * VLANE + (k % 4) * 4] = (uint8_t)q[k];
-                }
-            } else {
-                uint8_t by[4];
-#pragma unroll
-                for (int m = 0; m < 4; ++m)
-                    by[m] = (uint8_t)((q[2 * m] & 0x0f) | (q[2 * m + 1] & 0x0f) << 4);
-                if (which == 0) {
-                    uint32_t w = by[0] | by[1] << 8 | by[2] << 16 | (uint32_t)by[3] << 24;
-                    *reinterpret_cast<uint32_t *>(tile + ((j / KG) * BS + t) * (KG / 2) + (j % KG) / 2) = w;
-                } else {
-                    // Dim pair m of the chunk: VG = 8 keeps the chunk in one
-                    // lane group (words vk/2 .. +3); VG = 4 spans two (vk == 0).
-#pragma unroll
-                    for (int m = 0; m < 4; ++m) {
-                        const int jj = vk + 2 * m;
-                        vbase[(jj / VG) * VLANE + ((jj % VG) / 2) * 4] = by[m];
-                    }
-                }
-            }
+            place_chunk<QBITS>(tile, which, j, t, d, q);
         }
     }
 }
@@ -360,6 +367,72 @@ extern "C" int dlmk_kv_append(void *stream, void *k_pool, void *v_pool, const vo
     return DLMK_OK;
 }
 
+// Prefill-sized int8 appends: one work-group per run of 16 consecutive
+// source tokens, 512 threads (256 per pool; 16 lanes per token, RC chunks
+// each, so a token's max is a 16-lane shuffle reduction).  When the run's
+// slots fill one block in order, the codes are placed into an LDS image of
+// the block's tiles (every kv head) and the image is copied out with 16-byte
+// stores; otherwise each thread places its codes straight into the pool.
+constexpr int kQuantRunMaxKvDim = 1024;
+constexpr int64_t kQuantRunMinTokens = 512;
+
+template <int QBITS, typename S, int RC>
+__global__ __launch_bounds__(512) void kv_append_quant_run_kernel(
+    uint8_t *__restrict__ k_pool, uint8_t *__restrict__ v_pool, float *__restrict__ k_scales,
+    float *__restrict__ v_scales, const S *__restrict__ k_src, const S *__restrict__ v_src,
+    const int64_t *__restrict__ slots, int64_t n_tok, int num_kv_heads, int head_dim,
+    int64_t num_slots) {
+    constexpr int BS = 16;
+    __shared__ __attribute__((aligned(16))) uint8_t img[2][kQuantRunMaxKvDim * BS * QBITS / 8];
+    const int which = threadIdx.x >> 8, lt = threadIdx.x & 255, tt = lt >> 4, sub = lt & 15;
+    const int64_t tok0 = (int64_t)blockIdx.x * BS, tok = tok0 + tt;
+    const bool have = tok < n_tok;
+    const int d = head_dim, kv_dim = num_kv_heads * head_dim;
+    const float qmax = QBITS == 8 ? 127.f : 7.f;
+    const S *src = (which ? v_src : k_src) + (have ? tok : tok0) * kv_dim;
+    float x[RC][8];
+    float mx = 0.f;
+#pragma unroll
+    for (int i = 0; i < RC; ++i) {
+        load8(src + 8 * (sub + 16 * i), x[i]);
+#pragma unroll
+        for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(x[i][k]));
+    }
+#pragma unroll
+    for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    const int64_t slot = have ? slots[tok] : -1;
+    const int64_t slot0 = slots[tok0];  // tok0 < n_tok: the grid is ceil(n_tok / 16) runs
+    const bool in_run = have && slot0 >= 0 && slot0 % BS == 0 && slot0 + BS <= num_slots && slot == slot0 + tt;
+    const bool full = __syncthreads_and(in_run);
+    const bool valid = have && slot >= 0 && slot < num_slots;
+    const float scale = mx / qmax;
+    const float ok = scale > 0.f ? 1.f : 0.f;
+    if (valid && sub == 0) (which ? v_scales : k_scales)[slot] = ok != 0.f ? scale : 0.f;
+    uint8_t *pool = which ? v_pool : k_pool;
+    const int64_t tile_bytes = (int64_t)d * BS * QBITS / 8;
+    if (valid) {
+        const int64_t blk = slot / BS;
+        const int t = (int)(slot - blk * BS);
+#pragma unroll
+        for (int i = 0; i < RC; ++i) {
+            const int c = sub + 16 * i;
+            const int h = (8 * c) / d, j = 8 * c - h * d;
+            uint8_t *tile = full ? img[which] + h * tile_bytes : pool + (blk * num_kv_heads + h) * tile_bytes;
+            int q[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q[k] = quant_code(x[i][k], ok, scale, qmax) + (QBITS == 8 ? 128 : 8);
+            place_chunk<QBITS>(tile, which, j, t, d, q);
+        }
+    }
+    if (full) {  // uniform over the work-group
+        __syncthreads();
+        const int64_t units = num_kv_heads * tile_bytes / 16;
+        uint4 *dst = reinterpret_cast<uint4 *>(pool + (slot0 / BS) * num_kv_heads * tile_bytes);
+        const uint4 *from = reinterpret_cast<const uint4 *>(img[which]);
+        for (int64_t u = lt; u < units; u += 256) dst[u] = from[u];
+    }
+}
+
 extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, float *k_scales,
                                     float *v_scales, const void *k_src, const void *v_src,
                                     int src_dtype, const int64_t *slot_mapping, int64_t n_tok,
@@ -385,6 +458,13 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
         return dlmk::fail(DLMK_ERR_INVALID_ARG,
                           "dlmk_kv_append_quant: k_src / v_src not 16-byte aligned");
     const int nc = chunks_per_lane <= 1 ? 1 : chunks_per_lane <= 2 ? 2 : chunks_per_lane <= 4 ? 4 : 8;
+    // Runs of 16 tokens per work-group for prefill-sized int8 appends with
+    // kv_dim 512 or 1024 (4 or 8 chunks per lane): config 3's 2096 tokens
+    // 12.36 -> 11.56 us.  int4 measured slower that way (8.55 -> 11.59 us)
+    // and keeps one work-group per token.
+    const int rc = quant == DLMK_I8 && n_tok >= kQuantRunMinTokens &&
+                           (kv_dim == 512 || kv_dim == kQuantRunMaxKvDim)
+                       ? (int)(kv_dim / 8 / 16) : 0;
     const int64_t gx = n_tok;
     if (gx > 0x7fffffff) return dlmk::fail(DLMK_ERR_UNSUPPORTED, "dlmk_kv_append_quant: grid too large");
     auto s = (hipStream_t)stream;
@@ -394,7 +474,19 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
     hipLaunchKernelGGL((kv_append_quant_kernel<Q, S, NC>), dim3((unsigned)gx), dim3(256), 0, s, kp, \
                        vp, k_scales, v_scales, (const S *)k_src, (const S *)v_src, slot_mapping,  \
                        n_tok, num_kv_heads, head_dim, num_slots)
+#define DLMK_LAUNCH_RUN(Q, S, RC)                                                                    \
+    hipLaunchKernelGGL((kv_append_quant_run_kernel<Q, S, RC>), dim3((unsigned)dlmk::ceil_div(n_tok, (int64_t)16)), \
+                       dim3(512), 0, s, kp, vp, k_scales, v_scales, (const S *)k_src, (const S *)v_src,         \
+                       slot_mapping, n_tok, num_kv_heads, head_dim, num_slots)
 #define DLMK_LAUNCH(Q, S)                                             \
+    if (rc == 4) {                                                    \
+        DLMK_LAUNCH_RUN(Q, S, 4);                                     \
+        break;                                                        \
+    }                                                                 \
+    if (rc == 8) {                                                    \
+        DLMK_LAUNCH_RUN(Q, S, 8);                                     \
+        break;                                                        \
+    }                                                                 \
     switch (nc) {                                                     \
         case 1: DLMK_LAUNCH_NC(Q, S, 1); break;                       \
         case 2: DLMK_LAUNCH_NC(Q, S, 2); break;                       \
@@ -414,6 +506,7 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
                               src_dtype);
     }
 #undef DLMK_LAUNCH_NC
+#undef DLMK_LAUNCH_RUN
 #undef DLMK_LAUNCH
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return dlmk::fail((int)e, "dlmk_kv_append_quant launch: %s", hipGetErrorString(e));

@@ -94,19 +94,25 @@ def assert_pools_equal(kv, kp, vp, ksc, vsc, what):
 # ------------------------------------------------------------------ append
 
 @pytest.mark.parametrize("qname", ["int8", "int4"])
-@pytest.mark.parametrize("src,Hkv,d,ntok", [
-    ("f32", 8, 64, 200),    # config-1 geometry
-    ("f16", 8, 128, 700),   # config-2 geometry, prefill chunk + decode tokens
-    ("bf16", 2, 256, 90),
-    ("f16", 1, 64, 33),     # one head, smallest head dim
+@pytest.mark.parametrize("src,Hkv,d,ntok,ordered", [
+    ("f32", 8, 64, 200, False),    # config-1 geometry
+    ("f16", 8, 128, 700, False),   # config-2 geometry, prefill chunk + decode tokens
+    ("bf16", 2, 256, 90, False),
+    ("f16", 1, 64, 33, False),     # one head, smallest head dim
+    # >= 512 tokens in sequence order: 16-token runs that fill whole blocks
+    # (tiles composed in LDS) next to runs broken by skipped slots
+    ("f16", 8, 128, 700, True),    # kv_dim 1024
+    ("f32", 8, 64, 600, True),     # kv_dim 512
+    ("bf16", 4, 128, 530, True),   # kv_dim 512, ragged last run
 ])
-def test_kv_append_quant_bit_exact(oracle, torch_mod, ops, cuda, qname, src, Hkv, d, ntok):
+def test_kv_append_quant_bit_exact(oracle, torch_mod, ops, cuda, qname, src, Hkv, d, ntok, ordered):
     torch = torch_mod
-    banner(f"kv_append_quant {qname} src={src} Hkv={Hkv} d={d} ntok={ntok}")
+    banner(f"kv_append_quant {qname} src={src} Hkv={Hkv} d={d} ntok={ntok} ordered={ordered}")
     quant = _quant(oracle, qname)
     rng = np.random.default_rng(7 * ntok + d)
     nb, _, slots = layout(rng, [ntok])
-    slots = slots[rng.permutation(ntok)]  # tokens land in any order
+    if not ordered:
+        slots = slots[rng.permutation(ntok)]  # tokens land in any order
     slots[::29] = -1                      # skipped tokens
     slots[5] = nb * BS + 3                # out-of-pool slot: skipped
     k = tokens(rng, ntok, Hkv, d)
