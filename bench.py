@@ -568,7 +568,10 @@ def main():
     step_bytes = mean_attn_bytes + L * append_bytes(w, n_app)
     value = step_bytes / (step_ms * 1e-3) / 1e9
     attn_gbps = mean_attn_bytes / (attn_ms * 1e-3) / 1e9
+    # Context tokens one step attends over (summed over the batch, mean of the
+    # two rotating batches), and the per-sequence mean.
     ctx_tok = (batches[0].ctx.sum() + batches[1].ctx.sum()) / 2
+    ctx_mean = ctx_tok / w.batch
 
     result = {
         "metric": METRIC,
@@ -589,7 +592,8 @@ def main():
             "num_q_heads": w.hq, "num_kv_heads": w.hkv, "head_dim": w.d, "block_size": BS,
             "layers": w.layers, "batch": w.batch, "queries_per_seq": w.nq,
             "ctx": f"U[{w.ctx[0]},{w.ctx[1]}] seed {SEED}", "pool_blocks": pool_blocks,
-            "kv_quant": w.quant, "rotating_batches": 2, "mean_context_tokens": float(ctx_tok),
+            "kv_quant": w.quant, "rotating_batches": 2, "mean_context_tokens": round(float(ctx_mean), 1),
+            "context_tokens_per_step": float(ctx_tok),
             "appended_tokens_per_step": n_app, "parallelism": "single GPU",
         },
         "pct_of_hbm_peak": round(100 * value / HBM_PEAK_GBPS, 2),

@@ -22,7 +22,9 @@ BUILD_DIR = os.path.join(PKG, "_build")
 LIB_PATH = os.path.join(PKG, "libdlmk.so")
 
 ARCH = "gfx950"
-SOURCES = ["runtime.hip", "kv_cache.cpp", "kv_append.hip", "attention.hip", "blocks.hip",
+SOURCES = ["runtime.hip", "kv_cache.cpp", "kv_append.hip", "attention.hip", "attention_f32.hip",
+           "attention_f16.hip", "attention_bf16.hip", "attention_i8.hip", "attention_i4.hip",
+           "blocks.hip",
            "decode_block.hip"]
 
 # -packed-fp32-ops: keep the compiler from emitting packed FP32 VALU ops.

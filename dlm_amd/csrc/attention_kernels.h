@@ -1,0 +1,1335 @@
+#pragma once
+// Paged GQA decode attention kernels (dlmk_paged_decode_attention) for gfx950.
+// Included by attention.hip (entry points) and by one translation unit per
+// pool format (attention_<format>.hip), which instantiate the kernels.
+//
+// Replaces attention_kernel (src/gpu/kernels.cu:210-242: one thread per query
+// head, serial over a contiguous f32 history) and the CPU attention()
+// (src/forward/cpu.rs:1126-1151).  Same maths -- score = dot(q, k) * scale,
+// softmax over the visible positions, out = sum p * v -- evaluated as a
+// streaming, HBM-bound pass over the paged pools.
+//
+// Work decomposition (both kernels).  One work-group owns one (sequence, kv
+// head, partition of P tokens) and serves every query row that reads that kv
+// head: the GQA group times the num_q_per_seq verify queries (ROWS rows).  K/V
+// bytes of a partition are therefore read from HBM exactly once.  Partition
+// blocks are dealt to the NW wavefronts round-robin.  Each wave computes an
+// exact softmax over its own tokens (max over all its scores first, so no
+// rescaling), the waves are merged in LDS, and partitions of one sequence are
+// merged by log-sum-exp in a second kernel (a sequence whose context fits one
+// partition is finished by the first).  Everything runs in the log2 domain
+// with log2(e) folded into the scale.
+//
+// f16 / bf16 pools: matrix-core kernel.  Per 16-token block and wave:
+//   S^T (16 tokens x 16 rows) = K (16 x d) . Q^T (d x 16)
+//     v_mfma_f32_16x16x32_{f16,bf16}, d/32 steps.  A K-tile load of lane l
+//     (chunk row l/16 + 4i of token l%16, 16 bytes) is exactly the A operand,
+//     the query rows (zero-padded to 16) are the B operand.  The accumulator
+//     lands as lane l = (row l%16, tokens 4(l/16)..+3).
+//   O (16 rows x d) += P (16 x 16 tokens) . V (16 tokens x d)
+//     v_mfma_f32_16x16x16_{f16,bf16}, d/16 steps.  S^T's accumulator layout
+//     IS the A-operand layout of this product, so P never leaves registers;
+//     the B operand is 4 tokens x 1 dim = 8 contiguous bytes of the V tile
+//     [d][16].
+// int8 / int4 pools: the same kernel over f16 operands widened in registers
+//   from tiles laid out for 16-byte loads per lane (storage codecs below).
+// f32 pools: VALU kernel (dot products with FMA, cross-lane sums).
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <type_traits>
+
+#include "dlmk.h"
+#include "dlmk_internal.h"
+
+// Launch arguments shared by the entry points and the per-format dispatchers.
+namespace dlmk_attn {
+struct Args {
+    void *out;
+    int out_dtype;
+    const void *q;
+    void *k_pool, *v_pool;
+    const float *k_scales, *v_scales;  // quantized pools: one f32 per (block, token slot)
+    const void *k_new, *v_new;         // fused decode step: tokens appended in the same launch
+    const int32_t *tables, *ctx_lens;
+    int B, NQ, Hq, Hkv, max_blocks;
+    int64_t num_blocks;
+    float scale;
+    void *workspace;
+    int64_t ws_o_bytes;
+    hipStream_t stream;
+};
+
+// Per-format dispatchers (one translation unit each): launch the partition
+// kernel (and the combine kernel) for head_dim and GQA group a.Hq / a.Hkv.
+int dispatch_f32(const Args &a, int head_dim);
+int dispatch_f16(const Args &a, int head_dim);
+int dispatch_bf16(const Args &a, int head_dim);
+int dispatch_i8(const Args &a, int head_dim);
+int dispatch_i4(const Args &a, int head_dim);
+}  // namespace dlmk_attn
+
+namespace {
+
+using dlmk_attn::Args;
+
+constexpr int kBlock = 16;          // tokens per KV block (dlm: src/main.rs:455)
+constexpr int kMinPartition = 64;  // smallest partition of any kernel (sizes the workspace)
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Matrix-core kernel shape: waves per work-group, blocks per wave, prefetch
+// depth in tile loads (overridable at build time for tuning sweeps).
+#ifndef DLMK_MFMA_NW
+#define DLMK_MFMA_NW 4
+#endif
+#ifndef DLMK_MFMA_NB
+#define DLMK_MFMA_NB 16
+#endif
+#ifndef DLMK_MFMA_PD
+#define DLMK_MFMA_PD 2
+#endif
+// Minimum waves per SIMD for the quantized-pool kernels: half the bytes per
+// tile leave the per-tile latency chain exposed, so they trade registers for
+// occupancy.
+#ifndef DLMK_MFMA_QWAVES
+#define DLMK_MFMA_QWAVES 3
+#endif
+// Prefetch depth for int8 / int4 pools, whose tiles are 2x / 4x smaller.
+#ifndef DLMK_MFMA_PDQ
+#define DLMK_MFMA_PDQ 2
+#endif
+// Minimum waves per SIMD the register allocation must allow for every pool
+// format (0: per-format defaults above; a tuning override).
+#ifndef DLMK_MFMA_WPE
+#define DLMK_MFMA_WPE 0
+#endif
+// 1: stream K/V tiles with non-temporal loads (no reuse, keep them out of L2/MALL).
+#ifndef DLMK_MFMA_NT
+#define DLMK_MFMA_NT 1
+#endif
+
+// Pool stores of new tokens: non-temporal (written around the caches).  The
+// kernels stream the pools with non-temporal loads; read back that way, lines
+// written through the caches by an earlier launch measured several us slower
+// per launch at the 8B shape.
+template <typename V>
+__device__ __forceinline__ void pool_store(V *p, V v) {
+    __builtin_nontemporal_store(v, p);
+}
+
+template <typename V>
+__device__ __forceinline__ V stream_load(const V *p) {
+#if DLMK_MFMA_NT
+    return __builtin_nontemporal_load(p);
+#else
+    return *p;
+#endif
+}
+
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void store_out(void *out, int out_dtype, int64_t idx, float v) {
+    if (out_dtype == DLMK_F32) {
+        static_cast<float *>(out)[idx] = v;
+    } else if (out_dtype == DLMK_F16) {
+        static_cast<_Float16 *>(out)[idx] = (_Float16)v;
+    } else {
+        static_cast<__bf16 *>(out)[idx] = (__bf16)v;  // round to nearest even
+    }
+}
+
+template <int W>
+__device__ __forceinline__ float xor_sum(float v) {
+#pragma unroll
+    for (int o = 1; o < W; o <<= 1) v += __shfl_xor(v, o);
+    return v;
+}
+
+template <int W>
+__device__ __forceinline__ float xor_max(float v) {
+#pragma unroll
+    for (int o = 1; o < W; o <<= 1) v = fmaxf(v, __shfl_xor(v, o));
+    return v;
+}
+
+__device__ __forceinline__ int parts_of(int ctx, int P) { return ctx > P ? (ctx + P - 1) / P : 1; }
+
+// Shared epilogue: merge the NW waves' (m, l, O) of one work-group and either
+// finish the rows (single-partition sequence) or store the partition partial.
+// The ROWS x NW merge weights 2^(m_w - M) are computed once into LDS, so the
+// per-element pass is a plain weighted sum of the waves' O.
+template <int ROWS, int D, int NW, int GQA, int NQ>
+__device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][D],
+                                            const float (&ml_lds)[NW][ROWS][2], void *out,
+                                            int out_dtype, int seq, int kvh, int part,
+                                            int nparts, int num_q_heads, int max_parts,
+                                            float *ws_o, float *ws_ml) {
+    __shared__ float fac[ROWS][NW];
+    __shared__ float rowML[ROWS][2];
+    if (threadIdx.x < ROWS) {
+        const int r = threadIdx.x;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, ml_lds[w][r][0]);
+        float L = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float mw = ml_lds[w][r][0];
+            const float f = (M == -INFINITY || mw == -INFINITY) ? 0.f : exp2f(mw - M);
+            fac[r][w] = f;
+            L = fmaf(f, ml_lds[w][r][1], L);
+        }
+        rowML[r][0] = M;
+        rowML[r][1] = L;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < ROWS * D; idx += NW * 64) {
+        const int r = idx / D, d = idx - r * D;
+        float O = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) O = fmaf(fac[r][w], o_lds[w][r][d], O);
+        const float L = rowML[r][1];
+        const int j = r / GQA, h = kvh * GQA + r % GQA;
+        const int64_t row = (int64_t)(seq * NQ + j) * num_q_heads + h;
+        if (nparts == 1) {
+            store_out(out, out_dtype, row * D + d, L > 0.f ? O / L : 0.f);
+        } else {
+            const int64_t slot = row * max_parts + part;
+            ws_o[slot * D + d] = O;
+            if (d == 0) {
+                ws_ml[2 * slot] = rowML[r][0];
+                ws_ml[2 * slot + 1] = L;
+            }
+        }
+    }
+}
+
+// Fused decode step: the wave that owns block `blk` (logical block `lb`) of a
+// sequence writes the sequence's newest positions ctx - nq .. ctx - 1 that
+// fall in that block -- its kv head's K and V, the same bits dlmk_kv_append
+// would write.  Only this wave reads that tile in the launch.  The matrix-core
+// kernel takes the new values from k_new / v_new in registers and stores them
+// after its last tile load; the VALU kernel stores them before loading the
+// block, ordered by a wavefront-scope fence (a wave's global stores and later
+// loads of the same address are performed in program order).
+template <typename T, int D, bool NT>
+__device__ __forceinline__ void append_new_in_block(T *k_pool, T *v_pool, const T *k_new,
+                                                    const T *v_new, int64_t blk, int lb, int seq,
+                                                    int kvh, int num_kv_heads, int nq, int ctx,
+                                                    int lane) {
+    constexpr int X = 16 / sizeof(T);
+    constexpr int TILE = D * kBlock;
+    const int lo = max(ctx - nq, lb * kBlock), hi = min(ctx, lb * kBlock + kBlock);
+    const int64_t base = (blk * num_kv_heads + kvh) * TILE;
+    for (int e = lane; e < (hi - lo) * D; e += 64) {
+        const int p = lo + e / D, dim = e % D;
+        const int t = p - lb * kBlock, j = p - (ctx - nq);
+        const int64_t src = ((int64_t)(seq * nq + j) * num_kv_heads + kvh) * D + dim;
+        T *kd = &k_pool[base + (dim / X * kBlock + t) * X + dim % X];
+        T *vd = &v_pool[base + dim * kBlock + t];
+        if (NT) {
+            pool_store(kd, k_new[src]);
+            pool_store(vd, v_new[src]);
+        } else {
+            *kd = k_new[src];
+            *vd = v_new[src];
+        }
+    }
+}
+
+// 1: a wave processes its NB blocks last first (measured 100.4 against
+// 101.4 us a launch at the 8B shape, configs[1]).
+#ifndef DLMK_MFMA_REV
+#define DLMK_MFMA_REV 1
+#endif
+// Position of a wave's b-th processed block among its NB blocks.
+__device__ __forceinline__ int wave_block(int b, int nb) { return DLMK_MFMA_REV ? nb - 1 - b : b; }
+
+// Fused decode step, append work-group: threads tid, tid + nthreads, ...
+// store the K and V of sequence seq's newest nq positions for kv head kvh
+// (the bits dlmk_kv_append writes; masked or out-of-pool blocks skipped).
+template <typename T, int D>
+__device__ __forceinline__ void append_new_tokens(T *k_pool, T *v_pool, const T *k_new,
+                                                  const T *v_new, const int32_t *block_tables,
+                                                  const int32_t *ctx_lens, int seq, int kvh,
+                                                  int num_kv_heads, int nq, int max_blocks,
+                                                  int64_t num_blocks, int tid, int nthreads) {
+    constexpr int X = 16 / sizeof(T);
+    constexpr int TILE = D * kBlock;
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    for (int e = tid; e < nq * D; e += nthreads) {
+        const int j = e / D, dim = e % D, p = ctx - nq + j;
+        if (p < 0) continue;
+        const int64_t blk = block_tables[(int64_t)seq * max_blocks + p / kBlock];
+        if (blk < 0 || blk >= num_blocks) continue;
+        const int t = p % kBlock;
+        const int64_t base = (blk * num_kv_heads + kvh) * TILE;
+        const int64_t src = ((int64_t)(seq * nq + j) * num_kv_heads + kvh) * D + dim;
+        pool_store(&k_pool[base + (dim / X * kBlock + t) * X + dim % X], k_new[src]);
+        pool_store(&v_pool[base + dim * kBlock + t], v_new[src]);
+    }
+}
+
+__device__ __forceinline__ bool holds_new(int lb, int ctx, int nq) {
+    return lb * kBlock < ctx && lb * kBlock + kBlock > ctx - nq;
+}
+
+// ---------------------------------------------------------------------------
+// Matrix-core partition kernel (f16 / bf16 pools).
+// ---------------------------------------------------------------------------
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<_Float16> {
+    using elem = _Float16;
+    using x8 = f16x8;
+    using x4 = f16x4;
+    static __device__ __forceinline__ f32x4 qk(x8 a, x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 pv(x4 a, x4 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+    }
+};
+
+template <>
+struct Mfma<__bf16> {
+    using elem = __bf16;
+    using x8 = bf16x8;
+    using x4 = bf16x4;
+    static __device__ __forceinline__ f32x4 qk(x8 a, x8 b, f32x4 c) {
+        return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 pv(x4 a, x4 b, f32x4 c) {
+        typedef short s16x4 __attribute__((ext_vector_type(4)));
+        return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s16x4, a),
+                                                         __builtin_bit_cast(s16x4, b), c, 0, 0, 0);
+    }
+};
+
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+// Exact widening of small integer codes to f16 without conversions: the f16
+// with bit pattern 0x64uu is 1024 + uu for any byte uu, so a code c stored
+// offset binary as the unsigned byte (or nibble) c + b and placed under a
+// 0x64 high byte is the f16 value B + c with B = 1024 + b.  v_perm_b32 builds two such halves from bytes lo,
+// lo + 1 of w in one op.  The bias is not subtracted per element: the kernel
+// removes B * sum(q) from each score and B * sum(p) from each output row
+// (dot products are linear in the codes), which takes one VALU op per code
+// pair off the inner loops.  B + c is exact in f16 (|B + c| < 2048) and the
+// products are exact in the f32 accumulators, so the only extra rounding is
+// f32 accumulation of the larger partial sums (about 2^-24 * B relative to
+// the q or p magnitudes).
+template <int LO>
+__device__ __forceinline__ f16x2 biased_pair(uint32_t w) {
+    constexpr uint32_t sel = 0x04000400u | (uint32_t)LO | (uint32_t)(LO + 1) << 16;
+    return __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x64646464u, w, sel));
+}
+
+// Four biased byte codes (bytes 0..3 of w) -> f16x4 of B + c.
+__device__ __forceinline__ f16x4 biased4(uint32_t w) {
+    const f16x2 a = biased_pair<0>(w), b = biased_pair<2>(w);
+    return f16x4{a[0], a[1], b[0], b[1]};
+}
+
+// Storage codecs of the matrix-core kernel, one per pool format and head
+// dim D.  A codec says where a lane's K and V bytes sit in a (block, kv head)
+// tile and how they become MFMA operands:
+//   QK (S^T = K.Q^T, 16x16x32): step i takes 8 dims of token n (lane n + 16g)
+//     from K load i / SK, sub-step i % SK; q_chunk(i, g) is the 8-dim Q chunk
+//     those 8 K dims pair with, and q_op permutes a Q chunk into the order
+//     k_op emits K in (the dot product does not care which dims pair up, only
+//     that both sides agree).
+//   PV (O = P.V, 16x16x16): step k takes 4 tokens (4g .. 4g + 3) of one dim,
+//     from V load k / SV, sub-step k % SV; its output column n is dim
+//     v_dim(k, n).
+// Each lane loads 16 bytes per instruction wherever a tile holds that many
+// per lane: the int8 kernel with 8-byte K and 4-byte V loads reached 62% of
+// the read bandwidth a pure 16-byte read of the same tiles reaches 77%.
+//   Quantized codecs keep one f32 scale per token: K scales multiply the
+//     score, V scales multiply the probabilities (p * v_scale, 4 values per
+//     lane, instead of 32 widened values).  Codes widen to f16 exactly, as
+//     kBias + code (the kernel removes the bias).
+template <typename E, int D>
+struct CodecFloat {  // f16 / bf16 pools: K [d/8][16][8], V [d][16] elements
+    using QT = E;
+    using Op = Mfma<E>;
+    using KRaw = typename Op::x8;
+    using VRaw = typename Op::x4;
+    static constexpr bool kScaled = false;
+    static constexpr int kMinWaves = 1;  // memory-bound at the compiler's allocation
+    static constexpr float kBias = 0.f, kBiasK = 0.f;
+    static constexpr int64_t kTileBytes = (int64_t)D * kBlock * sizeof(E);
+    static constexpr int SK = 1, KL = D / 32, SV = 1, VL = D / 16;
+    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int i, int lane) {
+        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * i + lane);
+    }
+    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int lane) {
+        const int g = lane >> 4, n = lane & 15;
+        return stream_load(reinterpret_cast<const VRaw *>(tile) + ((16 * k + n) * kBlock + 4 * g) / 4);
+    }
+    static __device__ __forceinline__ int q_chunk(int i, int g) { return 4 * i + g; }
+    static __device__ __forceinline__ KRaw q_op(KRaw q) { return q; }
+    static __device__ __forceinline__ typename Op::x8 k_op(KRaw r, int) { return r; }
+    static __device__ __forceinline__ typename Op::x4 v_op(VRaw r, int) { return r; }
+    static __device__ __forceinline__ int v_dim(int k, int n) { return 16 * k + n; }
+};
+
+template <int D>
+using CodecF16 = CodecFloat<_Float16, D>;
+template <int D>
+using CodecBF16 = CodecFloat<__bf16, D>;
+
+// Quantized tiles (head dim a multiple of 64), int4 codes two to a byte with
+// the even element in the low nibble:
+//   K [D/KG][16 tokens][KG dims]: one lane load = KG dims of token n = SK
+//     QK steps (8 dims each);
+//   V [D/(16 VG)][4 token quads][16][VG dims][4 tokens]: one lane load = 4
+//     tokens x VG dims = VG PV steps, lane n holding dims VG n .. VG n + VG - 1
+//     of its quarter.
+template <int D>
+struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
+    using QT = _Float16;
+    using Op = Mfma<_Float16>;
+    using KRaw = u32x4;
+    using VRaw = u32x4;
+    static constexpr bool kScaled = true;
+    static constexpr float kBias = 1024.f + 128.f, kBiasK = kBias;  // bytes c + 128
+    static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;
+    static constexpr int64_t kTileBytes = (int64_t)D * kBlock;
+    static constexpr int SK = 2, KL = D / 64, SV = 4, VL = D / 64;
+    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int p, int lane) {
+        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * p + lane);
+    }
+    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int l, int lane) {
+        return stream_load(reinterpret_cast<const VRaw *>(tile) + 64 * l + lane);
+    }
+    static __device__ __forceinline__ int q_chunk(int i, int g) { return 8 * (i >> 1) + 2 * g + (i & 1); }
+    static __device__ __forceinline__ f16x8 q_op(f16x8 q) { return q; }
+    static __device__ __forceinline__ f16x8 k_op(KRaw r, int s) {
+        const f16x4 a = biased4(r[2 * s]), b = biased4(r[2 * s + 1]);
+        return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+    }
+    static __device__ __forceinline__ f16x4 v_op(VRaw r, int kk) { return biased4(r[kk]); }
+    static __device__ __forceinline__ int v_dim(int k, int n) { return 64 * (k >> 2) + 4 * n + (k & 3); }
+};
+
+template <int D>
+struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 64: 8-byte loads, a whole tile)
+    static constexpr bool kWide = D % 128 == 0;
+    static constexpr int KG = kWide ? 32 : 16, VG = kWide ? 8 : 4;
+    using QT = _Float16;
+    using Op = Mfma<_Float16>;
+    using KRaw = typename std::conditional<kWide, u32x4, u32x2>::type;
+    using VRaw = KRaw;
+    static constexpr bool kScaled = true;
+    // K codes are unbiased per element: with codes of at most 7 against a
+    // bias of 1032 the f32 cancellation in the scores, scaled by a large
+    // token's K scale, reaches the output tolerance.  V keeps the bias (its
+    // error is relative to p * v_scale, which the output is divided by).
+    static constexpr float kBias = 1024.f + 8.f, kBiasK = 0.f;  // nibbles c + 8
+    static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;
+    static constexpr int64_t kTileBytes = (int64_t)D * kBlock / 2;
+    static constexpr int SK = KG / 8, KL = D / (4 * KG), SV = VG, VL = D / (16 * VG);
+    static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int p, int lane) {
+        return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * p + lane);
+    }
+    static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int l, int lane) {
+        return stream_load(reinterpret_cast<const VRaw *>(tile) + 64 * l + lane);
+    }
+    static __device__ __forceinline__ int q_chunk(int i, int g) { return SK * (4 * (i / SK) + g) + i % SK; }
+    // k_op emits a word's elements in the order 0 2 4 6 1 3 5 7 (even nibbles, then odd).
+    static __device__ __forceinline__ f16x8 q_op(f16x8 q) {
+        return f16x8{q[0], q[2], q[4], q[6], q[1], q[3], q[5], q[7]};
+    }
+    static __device__ __forceinline__ f16x8 k_op(KRaw r, int s) {
+        const uint32_t x = r[s];  // nibbles c + 8
+        const f16x4 a = biased4(x & 0x0f0f0f0fu), b = biased4((x >> 4) & 0x0f0f0f0fu);
+        const f16x8 w = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        return w - (_Float16)kBias;
+    }
+    // Word kk / 2 holds dims kk & ~1 (low nibbles) and kk | 1 of 4 tokens.
+    static __device__ __forceinline__ f16x4 v_op(VRaw r, int kk) {
+        return biased4((r[kk >> 1] >> (4 * (kk & 1))) & 0x0f0f0f0fu);
+    }
+    static __device__ __forceinline__ int v_dim(int k, int n) { return 16 * VG * (k / VG) + VG * n + k % VG; }
+};
+
+#if DLMK_MFMA_WPE
+#define DLMK_MFMA_ATTRS __attribute__((amdgpu_waves_per_eu(DLMK_MFMA_WPE)))
+#else
+#define DLMK_MFMA_ATTRS __attribute__((amdgpu_waves_per_eu(C::kMinWaves)))
+#endif
+
+template <typename C, int D, int GQA, int NQ, int NW, int NB, int PD>
+__global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kernel(
+    void *__restrict__ out, int out_dtype, const typename C::QT *__restrict__ q,
+    uint8_t *__restrict__ k_pool, uint8_t *__restrict__ v_pool,
+    const float *__restrict__ k_scales, const float *__restrict__ v_scales,
+    const typename C::QT *__restrict__ k_new, const typename C::QT *__restrict__ v_new,
+    const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
+    int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
+    int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
+    using M = typename C::Op;
+    using x8 = typename M::x8;
+    using x4 = typename M::x4;
+    using PT = typename M::elem;
+    using QT = typename C::QT;
+    constexpr int ROWS = GQA * NQ;
+    constexpr int KI = D / 32;           // QK steps per block
+    constexpr int VN = D / 16;           // PV steps per block
+    constexpr int P = NW * NB * kBlock;  // tokens per work-group
+    constexpr int64_t TILE = C::kTileBytes;  // bytes per (block, kv head)
+    static_assert(ROWS <= 16 && D % 32 == 0, "unsupported geometry");
+
+    __shared__ float o_lds[NW][ROWS][D];
+    __shared__ float ml_lds[NW][ROWS][2];
+
+    // blockIdx.x = seq * num_kv_heads + kv head, blockIdx.y = partition: the
+    // dispatcher deals consecutive work-groups to the 8 XCDs round-robin, so
+    // with the (sequence, head) pair fastest every XCD gets the same mix of
+    // full and ragged partitions (partition-fastest would pin each XCD to one
+    // partition index, and late partitions exist only for long contexts).
+    // Partitions are dealt last index first: the high indices (long contexts
+    // only, mostly full) start early and the grid ends on partition 0, where
+    // the short sequences' small work-groups fill the drain (+1 point of HBM
+    // peak over first-index-first at the 8B shape).
+    if constexpr (!C::kScaled) {
+        // Fused decode step: the first row of the grid (dealt first) stores
+        // each (sequence, kv head)'s new tokens; the partition work-groups
+        // take them from k_new / v_new in registers instead of the pools.
+        // Issued at the head of the grid, the stores overlap the ramp of the
+        // read stream: 104.4 us a step at the 8B shape against 109.8 with the
+        // stores issued by the partition waves themselves (attention alone:
+        // 100.4 us).
+        if (k_new != nullptr && blockIdx.y == 0) {
+            append_new_tokens<QT, D>(reinterpret_cast<QT *>(k_pool), reinterpret_cast<QT *>(v_pool),
+                                     k_new, v_new, block_tables, ctx_lens, blockIdx.x / num_kv_heads,
+                                     blockIdx.x % num_kv_heads, num_kv_heads, NQ, max_blocks,
+                                     num_blocks, threadIdx.x, NW * 64);
+            return;
+        }
+    }
+    const int part = gridDim.y - 1 - blockIdx.y, kvh = blockIdx.x % num_kv_heads,
+              seq = blockIdx.x / num_kv_heads;
+    // A length beyond the table width is clamped: no read past a table row and
+    // no partition index past max_parts.
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    const int nparts = parts_of(ctx, P);
+    if (part >= nparts) return;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n = lane & 15;  // lane group, row (QK) / dim (PV) index
+    const int nblk_seq = (ctx + kBlock - 1) / kBlock;
+    const int32_t *table = block_tables + (int64_t)seq * max_blocks;
+
+    // Q^T operand: row n of the group, chunk q_chunk(i, g) (zeroed beyond
+    // ROWS below).  Lanes past ROWS load row n % ROWS, so the loads carry no
+    // branches (a masked load would make its first use wait for it).
+    x8 qb[KI];
+    {
+        const int r = n % ROWS;
+        const int j = r / GQA, h = kvh * GQA + r % GQA;
+        const x8 *qp = reinterpret_cast<const x8 *>(q + ((int64_t)(seq * NQ + j) * num_q_heads + h) * D);
+#pragma unroll
+        for (int i = 0; i < KI; ++i) qb[i] = qp[C::q_chunk(i, g)];
+    }
+    // Causal limit of this lane's row (verify query n / GQA).
+    const int limit = n < ROWS ? ctx - NQ + n / GQA + 1 : ctx;
+
+    // This wave's blocks: partition block b*NW + wave.  Blocks past the
+    // context (or with an id outside the pool) are masked, and their loads are
+    // pointed at the wave's first block so that every load can be issued
+    // unconditionally (a re-read hits L1/L2, not HBM): the loops below have no
+    // branches and the compiler can keep many loads in flight.
+    int lbs[NB];
+    int64_t blk[NB];
+    bool ok[NB];
+    int nvalid = 0;
+    // The table reads are unconditional (index clamped into the row), so the
+    // NB scalar loads go out back to back and share one wait; a guarded read
+    // per block would serialise NB memory round trips before the first tile.
+    int32_t raw[NB];
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int lb = part * (NW * NB) + wave_block(b, NB) * NW + wave;
+        raw[b] = table[max(min(lb, nblk_seq - 1), 0)];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int lb = part * (NW * NB) + wave_block(b, NB) * NW + wave;
+        const int64_t id = lb < nblk_seq ? (int64_t)raw[b] : -1;
+        lbs[b] = lb;
+        ok[b] = id >= 0 && id < num_blocks;
+        blk[b] = id;
+        nvalid += ok[b];
+    }
+
+    float m = -INFINITY, lsum = 0.f;
+    f32x4 accp = {0.f, 0.f, 0.f, 0.f};  // quantized pools: P row sums (rows 4g + j)
+    f32x4 acc[VN];
+#pragma unroll
+    for (int k = 0; k < VN; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Fused decode step: the newest NQ positions ctx - NQ .. ctx - 1 may not
+    // be in the pools yet (the append work-groups store them concurrently).
+    // They span at most two consecutive logical blocks, which belong to
+    // different waves (blocks are dealt round-robin), so a wave owns at most
+    // one of them (bnew).  The wave loads that block's tiles as usual, reads
+    // the new tokens' K/V from k_new / v_new alongside, and substitutes them
+    // lane by lane: the same bits the append writes, whichever bytes the tile
+    // load saw.
+    static_assert(NW >= 2, "new-token blocks must land on different waves");
+    int bnew = -1;
+    if constexpr (!C::kScaled) {
+        if (k_new != nullptr) {
+#pragma unroll
+            for (int b = 0; b < NB; ++b)
+                if (ok[b] && holds_new(lbs[b], ctx, NQ)) bnew = b;
+        }
+    }
+    bnew = __builtin_amdgcn_readfirstlane(bnew);
+    const int lb_new = part * (NW * NB) + wave_block(bnew, NB) * NW + wave;
+    const int first_new = ctx - NQ;
+    // K: lane (token n, group g) covers chunk rows 4i + g of token n.
+    const int jk = lb_new * kBlock + n - first_new;
+    const bool k_is_new = jk >= 0 && jk < NQ;
+    x8 knew[KI];
+    x4 vnew[VN];
+    if constexpr (!C::kScaled) {
+        if (bnew >= 0) {
+            const QT *kr = k_new + ((int64_t)(seq * NQ + min(max(jk, 0), NQ - 1)) * num_kv_heads + kvh) * D;
+#pragma unroll
+            for (int i = 0; i < KI; ++i) knew[i] = reinterpret_cast<const x8 *>(kr)[4 * i + g];
+            // V: lane (dim n of step k, group g) covers tokens 4g .. 4g + 3.
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int jv = min(max(lb_new * kBlock + 4 * g + e - first_new, 0), NQ - 1);
+                const QT *vr = v_new + ((int64_t)(seq * NQ + jv) * num_kv_heads + kvh) * D;
+#pragma unroll
+                for (int k = 0; k < VN; ++k) vnew[k][e] = vr[16 * k + n];
+            }
+        }
+    }
+
+    if (nvalid > 0) {
+        int64_t first = 0;
+#pragma unroll
+        for (int b = NB - 1; b >= 0; --b)
+            if (ok[b]) first = blk[b];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            if (!ok[b]) blk[b] = first;
+
+        // Software pipeline over the wave's 2*NB tile loads (K tiles of
+        // blocks 0..NB-1, then V tiles): load stage t + PD is issued before
+        // stage t is consumed, and scheduling barriers keep the compiler from
+        // sinking the loads next to their uses.
+        typename C::KRaw kb[NB][C::KL];
+        typename C::VRaw vb[NB][C::VL];
+        f32x4 ksc[NB], vsc[NB];
+        // A stage's scale load goes out before its code loads, fenced by a
+        // scheduling barrier: loads complete in issue order, so waiting for
+        // a scale never waits for a later stage's codes.
+        auto issue = [&](int t) {
+            if (t < NB) {
+                if constexpr (C::kScaled) {
+                    ksc[t] = *reinterpret_cast<const f32x4 *>(k_scales + blk[t] * kBlock + 4 * g);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                const uint8_t *kt = k_pool + (blk[t] * num_kv_heads + kvh) * TILE;
+#pragma unroll
+                for (int i = 0; i < C::KL; ++i) kb[t][i] = C::load_k(kt, i, lane);
+            } else if (t < 2 * NB) {
+                if constexpr (C::kScaled) {
+                    vsc[t - NB] = *reinterpret_cast<const f32x4 *>(v_scales + blk[t - NB] * kBlock + 4 * g);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                const uint8_t *vt = v_pool + (blk[t - NB] * num_kv_heads + kvh) * TILE;
+#pragma unroll
+                for (int l = 0; l < C::VL; ++l) vb[t - NB][l] = C::load_v(vt, l, lane);
+            }
+        };
+#pragma unroll
+        for (int t = 0; t < PD; ++t) issue(t);
+        __builtin_amdgcn_sched_barrier(0);
+        // Q operand in the order k_op emits K (zero rows past ROWS), after the
+        // first tile loads are out.
+#pragma unroll
+        for (int i = 0; i < KI; ++i) qb[i] = n < ROWS ? C::q_op(qb[i]) : x8{};
+        // Sum of row n's Q operand (as the MFMA sees it): the score bias is
+        // kBiasK * qsum.
+        float qsum = 0.f;
+        if constexpr (C::kBiasK != 0.f) {
+#pragma unroll
+            for (int i = 0; i < KI; ++i)
+#pragma unroll
+                for (int e = 0; e < 8; ++e) qsum += (float)qb[i][e];
+            qsum += __shfl_xor(qsum, 16);
+            qsum += __shfl_xor(qsum, 32);
+        }
+
+        // Scores S^T: s[b][j] = row n, token 4g + j of block b.
+        float s[NB][4];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            issue(b + PD);
+            __builtin_amdgcn_sched_barrier(0);
+            if constexpr (!C::kScaled) {
+                if (b == bnew) {
+#pragma unroll
+                    for (int i = 0; i < KI; ++i) kb[b][i] = k_is_new ? knew[i] : kb[b][i];
+                }
+            }
+            // Two accumulators (even / odd steps) halve the dependent MFMA chain.
+            f32x4 c = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < KI; i += 2) {
+                c = M::qk(C::k_op(kb[b][i / C::SK], i % C::SK), qb[i], c);
+                c1 = M::qk(C::k_op(kb[b][(i + 1) / C::SK], (i + 1) % C::SK), qb[i + 1], c1);
+            }
+            c += c1;
+            if constexpr (C::kScaled) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) c[j] = fmaf(-C::kBiasK, qsum, c[j]) * ksc[b][j];
+            }
+            // Every row sees all 16 tokens of this block (all blocks but a
+            // sequence's last, for one query): no masking (wave-uniform).
+            // Quantized pools only: the f16 kernel is memory-bound and
+            // measured 0.3 points slower with the branch.
+            const bool full = C::kScaled && __builtin_amdgcn_readfirstlane(
+                ok[b] && (lbs[b] + 1) * kBlock <= ctx - NQ + 1);
+            if (full) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[b][j] = c[j] * scale_log2;
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int pos = lbs[b] * kBlock + 4 * g + j;
+                    s[b][j] = (ok[b] && pos < limit) ? c[j] * scale_log2 : -INFINITY;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // Exact per-wave row max: own scores, then the 4 lane groups.
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m = fmaxf(m, s[b][j]);
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+
+        // O += P . V.  Float pools: P rounded to the operand type, and l sums
+        // the rounded P.  Quantized pools: the operand is p * v_scale (l sums
+        // p), so the widened codes need no per-element scaling.
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            issue(NB + b + PD);
+            __builtin_amdgcn_sched_barrier(0);
+            // Tokens at or past `valid` are outside the context (stale bytes,
+            // maybe NaN) or belong to a masked block (another block's bytes).
+            const int valid = __builtin_amdgcn_readfirstlane(ok[b] ? ctx - lbs[b] * kBlock : 0);
+            x4 pa;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                // v_exp_f32 directly: s - m <= 0 (or -inf, giving 0), and
+                // results below 2^-126 (flushed) do not matter next to the row max's 1.
+                const float p = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[b][j] - m);
+                if constexpr (C::kScaled) {
+                    // p is 0 there already; the select keeps a NaN scale out.
+                    pa[j] = (PT)(valid >= kBlock || 4 * g + j < valid ? p * vsc[b][j] : 0.f);
+                    lsum += p;
+                } else {
+                    const PT ph = (PT)p;
+                    pa[j] = ph;
+                    lsum += (float)ph;
+                }
+            }
+            if constexpr (C::kScaled) {
+                // Row sums of the operand the MFMA sees, subnormals included,
+                // on the matrix pipe: P . ones leaves row 4g + j's sum in
+                // column n of accp[j] (v_dot2_f32_f16 flushes subnormal f16
+                // and the bias turns any difference into kBias times that
+                // much output error).
+                const x4 ones = {(PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f};
+                accp = M::pv(pa, ones, accp);
+            }
+            typename M::x4 vo[VN];
+#pragma unroll
+            for (int k = 0; k < VN; ++k) vo[k] = C::v_op(vb[b][k / C::SV], k % C::SV);
+            if constexpr (!C::kScaled) {
+                if (b == bnew) {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const int jv = lb_new * kBlock + 4 * g + e - first_new;
+                        if (jv >= 0 && jv < NQ) {
+#pragma unroll
+                            for (int k = 0; k < VN; ++k) vo[k][e] = vnew[k][e];
+                        }
+                    }
+                }
+                // Float V can hold NaN past the context, and 0 * NaN is NaN:
+                // zero it.  A wave-uniform branch, taken only by partial blocks.
+                if (valid < kBlock) {
+#pragma unroll
+                    for (int k = 0; k < VN; ++k)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            vo[k][e] = 4 * g + e < valid ? vo[k][e] : (PT)0.f;
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < VN; ++k) acc[k] = M::pv(pa, vo[k], acc[k]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if constexpr (C::kScaled) {
+        // Output bias of row 4g + j: kBias * (row's P sum).
+        float ob[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) ob[j] = C::kBias * accp[j];
+#pragma unroll
+        for (int k = 0; k < VN; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[k][j] -= ob[j];
+    }
+
+    // acc[k][j] = O[row 4g + j][dim v_dim(k, n)].
+#pragma unroll
+    for (int k = 0; k < VN; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if (4 * g + j < ROWS) o_lds[wave][4 * g + j][C::v_dim(k, n)] = acc[k][j];
+    if (g == 0 && n < ROWS) {
+        ml_lds[wave][n][0] = m;
+        ml_lds[wave][n][1] = lsum;
+    }
+    __syncthreads();
+    merge_waves<ROWS, D, NW, GQA, NQ>(o_lds, ml_lds, out, out_dtype, seq, kvh, part, nparts,
+                                      num_q_heads, max_parts, ws_o, ws_ml);
+}
+
+// ---------------------------------------------------------------------------
+// VALU partition kernel (f32 pools).
+//   K tile [d/4][16][4]: load i of lane l is chunk row l/16 + 4i of token l%16,
+//     so one lane holds a 4-chunk partial dot for one token and the score
+//     needs a 4-way cross-lane sum (xor 16, xor 32).
+//   V tile [d][16]: load i of lane l is 4 consecutive tokens of one dim, so a
+//     lane's accumulator is ROWS x (loads) floats summed across the 4 lanes
+//     sharing a dim.
+// ---------------------------------------------------------------------------
+template <int D, int GQA, int NQ, int NW, int P>
+__global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
+    void *__restrict__ out, int out_dtype, const float *__restrict__ q, float *__restrict__ k_pool,
+    float *__restrict__ v_pool, const float *__restrict__ k_new, const float *__restrict__ v_new,
+    const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
+    int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
+    int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
+    constexpr int X = 4;                    // floats per 16-byte chunk
+    constexpr int CPL = D / X;              // chunks per token row
+    constexpr int KI = CPL / 4;             // 16-byte loads per lane per block (K and V alike)
+    constexpr int CPD = kBlock / X;         // V chunks per dim row of a tile
+    constexpr int ROWS = GQA * NQ;
+    constexpr int BPW = P / kBlock / NW;    // blocks per wave
+    constexpr int TILE = D * kBlock;
+    static_assert(CPL % 4 == 0 && BPW >= 1, "unsupported geometry");
+
+    __shared__ float p_lds[NW][BPW][ROWS][kBlock];
+    __shared__ float o_lds[NW][ROWS][D];
+    __shared__ float ml_lds[NW][ROWS][2];
+
+    // blockIdx.x = seq * num_kv_heads + kv head, blockIdx.y = partition: the
+    // dispatcher deals consecutive work-groups to the 8 XCDs round-robin, so
+    // with the (sequence, head) pair fastest every XCD gets the same mix of
+    // full and ragged partitions (partition-fastest would pin each XCD to one
+    // partition index, and late partitions exist only for long contexts).
+    // Partitions are dealt last index first: the high indices (long contexts
+    // only, mostly full) start early and the grid ends on partition 0, where
+    // the short sequences' small work-groups fill the drain (+1 point of HBM
+    // peak over first-index-first at the 8B shape).
+    const int part = gridDim.y - 1 - blockIdx.y, kvh = blockIdx.x % num_kv_heads,
+              seq = blockIdx.x / num_kv_heads;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int first_lb = part * (P / kBlock) + wave * BPW;
+    const int32_t *table = block_tables + (int64_t)seq * max_blocks;
+    // The table entries are read before the length (indices clamped into the
+    // row, not to the context), so the two reads overlap; entries past the
+    // context are masked below.
+    int32_t raw[BPW];
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) raw[b] = table[min(first_lb + b, max_blocks - 1)];
+    const int len = ctx_lens[seq];
+    // Both reads are used here, so the compiler issues them together and
+    // cannot sink the table reads past the early exit below.
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) asm volatile("" ::"s"(raw[b]), "s"(len));
+    const int ctx = min(len, max_blocks * kBlock);
+    const int nparts = parts_of(ctx, P);
+    if (part >= nparts) return;
+    const int nblk_seq = (ctx + kBlock - 1) / kBlock;
+
+    int64_t blk[BPW];
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) {
+        const int lb = first_lb + b;
+        int64_t id = lb < nblk_seq ? (int64_t)raw[b] : -1;
+        blk[b] = (id >= 0 && id < num_blocks) ? id : -1;
+    }
+    if (k_new != nullptr) {
+#pragma unroll
+        for (int b = 0; b < BPW; ++b)
+            if (blk[b] >= 0 && holds_new(first_lb + b, ctx, NQ))
+                append_new_in_block<float, D, false>(k_pool, v_pool, k_new, v_new, blk[b], first_lb + b,
+                                              seq, kvh, num_kv_heads, NQ, ctx, lane);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    }
+
+    uint4 kb[BPW][KI], vb[BPW][KI];
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) {
+        if (blk[b] >= 0) {
+            const int64_t base = (blk[b] * num_kv_heads + kvh) * TILE;
+            const uint4 *kp = reinterpret_cast<const uint4 *>(k_pool + base);
+            const uint4 *vp = reinterpret_cast<const uint4 *>(v_pool + base);
+#pragma unroll
+            for (int i = 0; i < KI; ++i) kb[b][i] = kp[64 * i + lane];
+#pragma unroll
+            for (int i = 0; i < KI; ++i) vb[b][i] = vp[64 * i + lane];
+        } else {
+#pragma unroll
+            for (int i = 0; i < KI; ++i) kb[b][i] = vb[b][i] = make_uint4(0, 0, 0, 0);
+        }
+    }
+
+    uint4 qr[ROWS][KI];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        const int j = r / GQA, h = kvh * GQA + r % GQA;
+        const uint4 *qp = reinterpret_cast<const uint4 *>(
+            q + ((int64_t)(seq * NQ + j) * num_q_heads + h) * D);
+#pragma unroll
+        for (int i = 0; i < KI; ++i) qr[r][i] = qp[(lane >> 4) + 4 * i];
+    }
+
+    const int tok = lane & 15;
+    float s[BPW][ROWS];
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            float acc = 0.f;
+#pragma unroll
+            for (int i = 0; i < KI; ++i) {
+                acc = fmaf(__uint_as_float(qr[r][i].x), __uint_as_float(kb[b][i].x), acc);
+                acc = fmaf(__uint_as_float(qr[r][i].y), __uint_as_float(kb[b][i].y), acc);
+                acc = fmaf(__uint_as_float(qr[r][i].z), __uint_as_float(kb[b][i].z), acc);
+                acc = fmaf(__uint_as_float(qr[r][i].w), __uint_as_float(kb[b][i].w), acc);
+            }
+            acc += __shfl_xor(acc, 16);
+            acc += __shfl_xor(acc, 32);
+            s[b][r] = acc;
+        }
+
+    float m[ROWS], l[ROWS];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r) {
+        const int limit = ctx - NQ + r / GQA + 1;
+        float mx = -INFINITY;
+#pragma unroll
+        for (int b = 0; b < BPW; ++b) {
+            const int pos = (first_lb + b) * kBlock + tok;
+            const bool vis = blk[b] >= 0 && pos < limit;
+            s[b][r] = vis ? s[b][r] * scale_log2 : -INFINITY;
+            mx = fmaxf(mx, s[b][r]);
+        }
+        mx = xor_max<16>(mx);
+        float sum = 0.f;
+#pragma unroll
+        for (int b = 0; b < BPW; ++b) {
+            const float p = mx == -INFINITY ? 0.f : exp2f(s[b][r] - mx);
+            s[b][r] = p;
+            sum += p;
+        }
+        m[r] = mx;
+        l[r] = xor_sum<16>(sum);
+    }
+
+#pragma unroll
+    for (int b = 0; b < BPW; ++b)
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+            if ((r & 3) == (lane >> 4)) p_lds[wave][b][r][tok] = s[b][r];
+    __syncthreads();
+
+    const int tg = lane % CPD;
+    float acc[ROWS][KI];
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int i = 0; i < KI; ++i) acc[r][i] = 0.f;
+
+#pragma unroll
+    for (int b = 0; b < BPW; ++b) {
+        if (blk[b] < 0) continue;
+        float pr[ROWS][X];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+            for (int e = 0; e < X; ++e) pr[r][e] = p_lds[wave][b][r][tg * X + e];
+        const int valid = ctx - (first_lb + b) * kBlock;
+#pragma unroll
+        for (int i = 0; i < KI; ++i) {
+            float v[X] = {__uint_as_float(vb[b][i].x), __uint_as_float(vb[b][i].y),
+                          __uint_as_float(vb[b][i].z), __uint_as_float(vb[b][i].w)};
+            if (valid < kBlock) {
+#pragma unroll
+                for (int e = 0; e < X; ++e)
+                    if (tg * X + e >= valid) v[e] = 0.f;
+            }
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                for (int e = 0; e < X; ++e) acc[r][i] = fmaf(pr[r][e], v[e], acc[r][i]);
+        }
+    }
+
+#pragma unroll
+    for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+        for (int i = 0; i < KI; ++i) acc[r][i] = xor_sum<CPD>(acc[r][i]);
+
+    if (tg == 0) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+            for (int i = 0; i < KI; ++i) o_lds[wave][r][(64 * i + lane) / CPD] = acc[r][i];
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) {
+            ml_lds[wave][r][0] = m[r];
+            ml_lds[wave][r][1] = l[r];
+        }
+    }
+    __syncthreads();
+    merge_waves<ROWS, D, NW, GQA, NQ>(o_lds, ml_lds, out, out_dtype, seq, kvh, part, nparts,
+                                      num_q_heads, max_parts, ws_o, ws_ml);
+}
+
+// ---------------------------------------------------------------------------
+// Pass 2: log-sum-exp merge of a sequence's partitions.  Rows of up to
+// kCombineBatch partitions: one wave per (query row, sequence), kCombineWaves
+// rows per work-group.
+// ---------------------------------------------------------------------------
+constexpr int kCombineWaves = 4;
+constexpr int kCombineBatch = 8;
+
+template <int D>
+__global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wave_kernel(
+    void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
+    const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
+    int max_blocks, int partition, int max_parts) {
+    constexpr int DPL = D / 64;  // dims per lane
+    constexpr int B = kCombineBatch;  // partitions loaded per batch
+    // One wave per (sequence, query row), kCombineWaves rows per work-group:
+    // the wave folds all of the row's partitions itself (online rescale), so
+    // no cross-wave merge and a quarter of the work-groups of one per row.
+    const int seq = blockIdx.y;
+    const int lane = threadIdx.x & 63;
+    const int r = blockIdx.x * kCombineWaves + (threadIdx.x >> 6);
+    if (r >= rows_per_seq) return;
+    const int64_t row = (int64_t)seq * rows_per_seq + r;
+    const float *ml = ws_ml + 2 * row * max_parts;
+    const float *o = ws_o + row * max_parts * D;
+
+    float mb[B], lb[B], ob[B][DPL];
+    auto load = [&](int p0, int last) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int p = min(p0 + i, last);
+            mb[i] = ml[2 * p];
+            lb[i] = ml[2 * p + 1];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) ob[i][k] = o[(int64_t)p * D + lane + 64 * k];
+        }
+    };
+    // The first batch is read before the context length is known (every
+    // slot below max_parts exists; only those below nparts are used), so
+    // rows of up to B partitions cost one memory round trip.
+    load(0, max_parts - 1);
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    const int nparts = parts_of(ctx, partition);
+    if (nparts == 1) return;
+
+    float m = -INFINITY, L = 0.f, O[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) O[k] = 0.f;
+    for (int p0 = 0;;) {
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            if (p0 + i >= nparts) break;
+            const float mn = fmaxf(m, mb[i]);
+            if (mn == -INFINITY) continue;  // both empty
+            const float fa = m == -INFINITY ? 0.f : exp2f(m - mn);
+            const float fb = mb[i] == -INFINITY ? 0.f : exp2f(mb[i] - mn);
+            L = fa * L + fb * lb[i];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) O[k] = fa * O[k] + fb * ob[i][k];
+            m = mn;
+        }
+        p0 += B;
+        if (p0 >= nparts) break;
+        load(p0, nparts - 1);
+    }
+#pragma unroll
+    for (int k = 0; k < DPL; ++k)
+        store_out(out, out_dtype, row * D + lane + 64 * k, L > 0.f ? O[k] / L : 0.f);
+}
+
+// Rows of more than kCombineBatch partitions: one work-group of
+// kCombineWaves waves per (query row, sequence).  Wave w loads its first
+// partition (w) before the context length arrives, folds w + W, ... in
+// batches with an online rescale, and the waves merge once in LDS.
+template <int D>
+__global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kernel(
+    void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
+    const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
+    int max_blocks, int partition, int max_parts) {
+    constexpr int W = kCombineWaves;
+    constexpr int DPL = D / 64;  // dims per lane
+    __shared__ float wml[W][2];
+    __shared__ float so[W][D + 1];
+    const int seq = blockIdx.y;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int64_t row = (int64_t)seq * rows_per_seq + blockIdx.x;
+    const float *ml = ws_ml + 2 * row * max_parts;
+    const float *o = ws_o + row * max_parts * D;
+
+    // Wave w's first partition (w) is loaded before the context length is
+    // known (the slot exists for every w < max_parts; it is used only if
+    // w < nparts), so the common case -- at most W partitions -- costs one
+    // memory round trip.  Further partitions w + W, ... fold in with an
+    // online rescale; the W waves then merge once.
+    float m = -INFINITY, L = 0.f, O[DPL];
+    float m0 = -INFINITY, l0 = 0.f, o0[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) O[k] = o0[k] = 0.f;
+    if (wave < max_parts) {
+        m0 = ml[2 * wave];
+        l0 = ml[2 * wave + 1];
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) o0[k] = o[(int64_t)wave * D + lane + 64 * k];
+    }
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    const int nparts = parts_of(ctx, partition);
+    if (nparts == 1) return;
+    if (wave < nparts) {
+        m = m0;
+        L = l0;
+#pragma unroll
+        for (int k = 0; k < DPL; ++k) O[k] = o0[k];
+    }
+    // Later partitions in batches of B per wave: all of a batch's loads go
+    // out before any is folded (indices clamped into the row, folds skipped
+    // past nparts).
+    constexpr int B = 8;
+    for (int p0 = wave + W; p0 < nparts; p0 += B * W) {
+        float mb[B], lb[B], ob[B][DPL];
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            const int p = min(p0 + i * W, nparts - 1);
+            mb[i] = ml[2 * p];
+            lb[i] = ml[2 * p + 1];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) ob[i][k] = o[(int64_t)p * D + lane + 64 * k];
+        }
+#pragma unroll
+        for (int i = 0; i < B; ++i) {
+            if (p0 + i * W >= nparts) break;
+            const float mn = fmaxf(m, mb[i]);
+            if (mn == -INFINITY) continue;  // both empty
+            const float fa = m == -INFINITY ? 0.f : exp2f(m - mn);
+            const float fb = mb[i] == -INFINITY ? 0.f : exp2f(mb[i] - mn);
+            L = fa * L + fb * lb[i];
+#pragma unroll
+            for (int k = 0; k < DPL; ++k) O[k] = fa * O[k] + fb * ob[i][k];
+            m = mn;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) so[wave][lane + 64 * k] = O[k];
+    if (lane == 0) {
+        wml[wave][0] = m;
+        wml[wave][1] = L;
+    }
+    __syncthreads();
+    float M = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < W; ++w) M = fmaxf(M, wml[w][0]);
+    float fw[W], Lt = 0.f;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+        fw[w] = (M == -INFINITY || wml[w][0] == -INFINITY) ? 0.f : exp2f(wml[w][0] - M);
+        Lt = fmaf(fw[w], wml[w][1], Lt);
+    }
+    for (int d = threadIdx.x; d < D; d += 64 * W) {
+        float Ot = 0.f;
+#pragma unroll
+        for (int w = 0; w < W; ++w) Ot = fmaf(fw[w], so[w][d], Ot);
+        store_out(out, out_dtype, row * D + d, Lt > 0.f ? Ot / Lt : 0.f);
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Host dispatch.
+// ---------------------------------------------------------------------------
+
+inline int64_t parts_for(int max_blocks, int partition) {
+    int64_t tokens = (int64_t)max_blocks * kBlock;
+    return tokens > partition ? dlmk::ceil_div(tokens, partition) : 1;
+}
+
+// Launches the partition kernel through `launch(grid, max_parts, ws_o, ws_ml)`,
+// then the combine kernel when a sequence can span several partitions.
+template <int D, typename Launch>
+int launch_pair(const Args &a, int partition, Launch launch) {
+    const int max_parts = (int)parts_for(a.max_blocks, partition);
+    float *ws_o = nullptr, *ws_ml = nullptr;
+    if (max_parts > 1) {
+        ws_o = static_cast<float *>(a.workspace);
+        ws_ml = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + a.ws_o_bytes);
+    }
+    launch(dim3((unsigned)(a.B * a.Hkv), (unsigned)max_parts), max_parts, ws_o, ws_ml);
+    // Rows of up to kCombineBatch partitions: a wave per row (config 5
+    // 64.9 -> 66.2%); longer rows: a work-group per row, whose four waves
+    // share the row's partitions (the wave-per-row kernel was 0.8 points
+    // slower at config 4's 32 partitions and 2.9 us slower in the decode
+    // block's 32).
+    if (max_parts > kCombineBatch)
+        hipLaunchKernelGGL(paged_attn_combine_wg_kernel<D>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
+                           dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
+                           a.NQ * a.Hq, a.max_blocks, partition, max_parts);
+    else if (max_parts > 1)
+        hipLaunchKernelGGL(paged_attn_combine_wave_kernel<D>,
+                           dim3((unsigned)((a.NQ * a.Hq + kCombineWaves - 1) / kCombineWaves), (unsigned)a.B),
+                           dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
+                           a.NQ * a.Hq, a.max_blocks, partition, max_parts);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return dlmk::fail((int)e, "paged attention launch: %s", hipGetErrorString(e));
+    return DLMK_OK;
+}
+
+// Matrix-core path: NW waves x NB blocks per partition, pool format C.
+template <typename C, int D, int GQA, int NQ>
+int launch_mfma(const Args &a) {
+    constexpr int NW = DLMK_MFMA_NW, NB = DLMK_MFMA_NB;
+    constexpr int PD = C::kScaled ? DLMK_MFMA_PDQ : DLMK_MFMA_PD;
+    static_assert(NW * NB * kBlock >= kMinPartition, "partition below the workspace bound");
+    using QT = typename C::QT;
+    return launch_pair<D>(a, NW * NB * kBlock, [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
+        // Fused decode step: one more grid row of append work-groups.
+        if (!C::kScaled && a.k_new != nullptr) grid.y += 1;
+        hipLaunchKernelGGL((paged_attn_mfma_kernel<C, D, GQA, NQ, NW, NB, PD>), grid, dim3(NW * 64), 0,
+                           a.stream, a.out, a.out_dtype, static_cast<const QT *>(a.q),
+                           static_cast<uint8_t *>(a.k_pool), static_cast<uint8_t *>(a.v_pool),
+                           a.k_scales, a.v_scales, static_cast<const QT *>(a.k_new),
+                           static_cast<const QT *>(a.v_new), a.tables, a.ctx_lens, a.Hq, a.Hkv,
+                           a.max_blocks, a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
+    });
+}
+
+// 256-token partitions when that grid fills the chip; otherwise smaller
+// partitions, as large as still give kValuMinGrid work-groups (a single
+// decoding sequence, as in dlmk_decode_block_paged, has num_kv_heads x
+// ctx / 256 work-groups: 64 at the 8B shape and ctx 2048).  Measured at the
+// decode block's shape (ctx 2048: 128 work-groups with 128-token partitions)
+// 128-token beat 64-token partitions by 1.1 us a layer; at config 1's
+// (ctx 640: 40 of them) 64-token ones won by 0.4 us.
+constexpr int64_t kValuSmallGrid = 1024;  // work-groups
+constexpr int64_t kValuMinGrid = 128;
+
+template <int D, int GQA, int NQ, int NW, int P>
+int launch_valu_p(const Args &a) {
+    static_assert(P >= kMinPartition, "partition below the workspace bound");
+    return launch_pair<D>(a, P, [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
+        hipLaunchKernelGGL((paged_attn_valu_kernel<D, GQA, NQ, NW, P>), grid, dim3(NW * 64), 0, a.stream,
+                           a.out, a.out_dtype, static_cast<const float *>(a.q),
+                           static_cast<float *>(a.k_pool), static_cast<float *>(a.v_pool),
+                           static_cast<const float *>(a.k_new), static_cast<const float *>(a.v_new),
+                           a.tables, a.ctx_lens, a.Hq, a.Hkv, a.max_blocks, a.num_blocks,
+                           a.scale * kLog2e, max_parts, ws_o, ws_ml);
+    });
+}
+
+template <int D, int GQA, int NQ>
+int launch_valu(const Args &a) {
+    constexpr int NW = GQA * NQ <= 4 ? 4 : 8;
+    const auto grid = [&](int p) { return (int64_t)a.B * a.Hkv * parts_for(a.max_blocks, p); };
+    if (grid(256) >= kValuSmallGrid) return launch_valu_p<D, GQA, NQ, NW, 256>(a);
+    if (grid(128) >= kValuMinGrid) return launch_valu_p<D, GQA, NQ, NW, 128>(a);
+    return launch_valu_p<D, GQA, NQ, NW, NW * kBlock>(a);
+}
+
+inline int unsupported_rows(int gqa, int nq) {
+    return dlmk::fail(DLMK_ERR_UNSUPPORTED,
+                      "paged attention: no kernel for GQA group %d x %d queries", gqa, nq);
+}
+
+template <template <int> class CD, int D>
+int dispatch_mfma(const Args &a, int gqa) {
+    using C = CD<D>;
+    switch (gqa * 16 + a.NQ) {
+        case 1 * 16 + 1: return launch_mfma<C, D, 1, 1>(a);
+        case 1 * 16 + 2: return launch_mfma<C, D, 1, 2>(a);
+        case 1 * 16 + 4: return launch_mfma<C, D, 1, 4>(a);
+        case 2 * 16 + 1: return launch_mfma<C, D, 2, 1>(a);
+        case 2 * 16 + 2: return launch_mfma<C, D, 2, 2>(a);
+        case 2 * 16 + 4: return launch_mfma<C, D, 2, 4>(a);
+        case 4 * 16 + 1: return launch_mfma<C, D, 4, 1>(a);
+        case 4 * 16 + 2: return launch_mfma<C, D, 4, 2>(a);
+        case 4 * 16 + 4: return launch_mfma<C, D, 4, 4>(a);
+        case 8 * 16 + 1: return launch_mfma<C, D, 8, 1>(a);
+        case 8 * 16 + 2: return launch_mfma<C, D, 8, 2>(a);
+        case 16 * 16 + 1: return launch_mfma<C, D, 16, 1>(a);
+        default: return unsupported_rows(gqa, a.NQ);
+    }
+}
+
+template <int D>
+int dispatch_valu(const Args &a, int gqa) {
+    switch (gqa * 16 + a.NQ) {
+        case 1 * 16 + 1: return launch_valu<D, 1, 1>(a);
+        case 1 * 16 + 2: return launch_valu<D, 1, 2>(a);
+        case 1 * 16 + 4: return launch_valu<D, 1, 4>(a);
+        case 2 * 16 + 1: return launch_valu<D, 2, 1>(a);
+        case 2 * 16 + 2: return launch_valu<D, 2, 2>(a);
+        case 2 * 16 + 4: return launch_valu<D, 2, 4>(a);
+        case 4 * 16 + 1: return launch_valu<D, 4, 1>(a);
+        case 4 * 16 + 2: return launch_valu<D, 4, 2>(a);
+        case 8 * 16 + 1: return launch_valu<D, 8, 1>(a);
+        default: return unsupported_rows(gqa, a.NQ);
+    }
+}
+
+inline int bad_dim(int head_dim, const char *dims) {
+    return dlmk::fail(DLMK_ERR_UNSUPPORTED,
+                      "paged attention: head_dim %d unsupported for this dtype (%s)",
+                      head_dim, dims);
+}
+
+}  // namespace

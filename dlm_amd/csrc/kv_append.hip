@@ -23,6 +23,26 @@ namespace {
 
 constexpr int kThreads = 256;
 
+#ifndef DLMK_STORE_NT
+#define DLMK_STORE_NT 1
+#endif
+// Pool stores: non-temporal (write around the caches).  The attention kernels
+// stream the pools with non-temporal loads, and those measured ~5 us slower
+// per launch at the 8B shape when the lines they read were written through
+// the caches by the step before.
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+template <typename V>
+__device__ __forceinline__ void pool_store(V *p, V v) {
+#if DLMK_STORE_NT
+    __builtin_nontemporal_store(v, p);
+#else
+    *p = v;
+#endif
+}
+__device__ __forceinline__ void pool_store(uint4 *p, uint4 v) {
+    pool_store(reinterpret_cast<u32x4 *>(p), __builtin_bit_cast(u32x4, v));
+}
+
 template <int EB>
 struct Bits;
 template <>
@@ -64,13 +84,13 @@ __global__ __launch_bounds__(kThreads) void kv_append_kernel(
     for (int c = 0; c < CPT; ++c) {
         const int chunk = chunk0 + c;
         // K tile [d/X][bs][X]: chunk row `chunk`, token t.
-        *reinterpret_cast<uint4 *>(k_pool + tile + ((int64_t)chunk * block_size + t) * 16) = kc[c];
+        pool_store(reinterpret_cast<uint4 *>(k_pool + tile + ((int64_t)chunk * block_size + t) * 16), kc[c]);
         // V tile [d][bs]: element (dim, t).
         E ve[X];
         __builtin_memcpy(ve, &vc[c], 16);
         E *vrow = reinterpret_cast<E *>(v_pool + tile) + (int64_t)chunk * X * block_size + t;
 #pragma unroll
-        for (int e = 0; e < X; ++e) vrow[(int64_t)e * block_size] = ve[e];
+        for (int e = 0; e < X; ++e) pool_store(&vrow[(int64_t)e * block_size], ve[e]);
     }
 }
 

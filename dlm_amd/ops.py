@@ -380,10 +380,60 @@ def scatter_blocks(k_pool, v_pool, staging, block_ids, block_bytes: int, stream=
                                     nb))
 
 
-def _pinned(host: torch.Tensor, n: int, block_bytes: int) -> None:
-    if host.device.type != "cpu" or not host.is_pinned() or not host.is_contiguous():
-        raise ValueError("host buffer must be contiguous pinned CPU memory")
-    if host.numel() * host.element_size() < 2 * n * block_bytes:
+class PinnedBuffer:
+    """Page-locked host staging from dlmk_alloc_pinned (dlm's PinnedBuffer,
+    src/memory/pinned.rs:38-112): at least `nbytes` bytes, rounded up to whole
+    pages and zero-initialised; a zero-byte request raises (DlmError::HostAlloc
+    there).  Freed with dlmk_free_pinned by free(), on context exit or when
+    the object is collected."""
+
+    PAGE = 4096
+
+    def __init__(self, nbytes: int):
+        import ctypes
+        p = ctypes.c_void_p()
+        check(lib().dlmk_alloc_pinned(ctypes.byref(p), int(nbytes)))
+        self._ptr = p.value
+        self.len = int(nbytes)
+        self.capacity = -(-self.len // self.PAGE) * self.PAGE
+
+    def data_ptr(self) -> int:
+        if not self._ptr:
+            raise ValueError("pinned buffer already freed")
+        return self._ptr
+
+    def numpy(self):
+        """A uint8 NumPy view of the first `len` bytes (valid until free())."""
+        import ctypes
+        import numpy as np
+        return np.ctypeslib.as_array((ctypes.c_uint8 * self.len).from_address(self.data_ptr()))
+
+    def free(self) -> None:
+        if self._ptr:
+            ptr, self._ptr = self._ptr, None
+            check(lib().dlmk_free_pinned(ptr))
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.free()
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def _pinned(host, n: int, block_bytes: int) -> None:
+    if isinstance(host, PinnedBuffer):
+        nbytes = host.len
+    else:
+        if host.device.type != "cpu" or not host.is_pinned() or not host.is_contiguous():
+            raise ValueError("host buffer must be contiguous pinned CPU memory")
+        nbytes = host.numel() * host.element_size()
+    if nbytes < 2 * n * block_bytes:
         raise ValueError("host buffer too small")
 
 

@@ -338,7 +338,11 @@ int dlmk_decode_block_paged(
     int max_blocks_per_seq, int num_positions, int position, void *workspace,
     size_t workspace_bytes);
 
-/* Pinned host memory, PinnedBuffer (src/memory/pinned.rs:38-112) analogue. */
+/* Pinned host memory, PinnedBuffer (src/memory/pinned.rs:38-112) analogue.
+ * dlmk_alloc_pinned: page-locked, zero-initialised, rounded up to whole 4 KiB
+ * pages (PinnedBuffer::with_len, pinned.rs:59-67); bytes == 0 returns
+ * DLMK_ERR_INVALID_ARG (DlmError::HostAlloc there) and sets *ptr to NULL, as
+ * does any failure.  dlmk_free_pinned(NULL) is a no-op returning 0. */
 int dlmk_alloc_pinned(void **ptr, size_t bytes);
 int dlmk_free_pinned(void *ptr);
 

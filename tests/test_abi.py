@@ -78,3 +78,21 @@ def test_workspace_size_formula(dlmk):
     o = rows * parts * 128 * 4
     assert dlmk.dlmk_paged_attention_workspace_size(64, 1, 32, 128, 16, 256) == \
         (o + 255) // 256 * 256 + rows * parts * 8
+
+
+def test_alloc_pinned_error_paths(dlmk):
+    # PinnedBuffer::with_len(0) is DlmError::HostAlloc (src/memory/pinned.rs:59-66):
+    # here DLMK_ERR_INVALID_ARG, *ptr NULL and a last-error string.  No GPU call
+    # is made on these paths.
+    p = C.c_void_p(1234)
+    assert dlmk.dlmk_alloc_pinned(C.byref(p), 0) == _lib.DLMK_ERR_INVALID_ARG
+    assert p.value is None
+    assert "zero bytes" in _lib.last_error()
+    assert dlmk.dlmk_alloc_pinned(None, 16) == _lib.DLMK_ERR_INVALID_ARG
+    assert "null out pointer" in _lib.last_error()
+    assert dlmk.dlmk_alloc_pinned(C.byref(p), 2**64 - 1) == _lib.DLMK_ERR_INVALID_ARG
+    assert p.value is None
+    assert dlmk.dlmk_free_pinned(None) == 0
+    from dlm_amd import ops
+    with pytest.raises(_lib.DlmkError):
+        ops.PinnedBuffer(0)

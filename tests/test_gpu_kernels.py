@@ -362,3 +362,39 @@ def test_gather_scatter_swap_round_trip(oracle, torch_mod, ops, cuda):
     torch.cuda.synchronize()
     assert np.array_equal(k_dev.cpu().numpy(), kp)
     assert np.array_equal(v_dev.cpu().numpy(), vp)
+
+
+def test_swap_through_library_pinned_buffer(oracle, torch_mod, ops, cuda):
+    """Swap staging in host memory from dlmk_alloc_pinned (dlm's PinnedBuffer,
+    src/memory/pinned.rs:38-112) instead of torch's pinned allocator: starts
+    zeroed, rounds up to whole pages, swap-out then swap-in is the identity on
+    the evicted blocks' bytes, and dlmk_free_pinned releases it."""
+    torch = torch_mod
+    banner("swap through dlmk_alloc_pinned")
+    rng = np.random.default_rng(34)
+    nb, bb = 200, 8 * 16 * 64 * 4  # f32 blocks of the config-1 shape
+    kp = rng.integers(0, 256, nb * bb, dtype=np.uint8)
+    vp = rng.integers(0, 256, nb * bb, dtype=np.uint8)
+    ids = rng.permutation(nb)[:50].astype(np.int32)
+    k_dev, v_dev = to_dev(torch, kp, cuda), to_dev(torch, vp, cuda)
+    ids_dev = to_dev(torch, ids, cuda)
+    nbytes = 2 * len(ids) * bb + 100  # not a page multiple
+    buf = ops.PinnedBuffer(nbytes)
+    assert buf.capacity % 4096 == 0 and buf.capacity >= nbytes
+    host = buf.numpy()
+    assert host.size == nbytes and not host.any()  # zero-initialised
+    staging = torch.empty(2 * len(ids) * bb, dtype=torch.uint8, device=cuda)
+    ops.swap_out(buf, k_dev, v_dev, ids_dev, bb, staging)
+    torch.cuda.synchronize()
+    assert np.array_equal(host[:2 * len(ids) * bb], oracle.gather_blocks(kp, vp, ids, bb))
+    assert not host[2 * len(ids) * bb:].any()
+    k_dev.view(nb, bb)[ids_dev.long()] = 0
+    v_dev.view(nb, bb)[ids_dev.long()] = 0
+    ops.swap_in(k_dev, v_dev, buf, ids_dev, bb, staging)
+    torch.cuda.synchronize()
+    assert np.array_equal(k_dev.cpu().numpy(), kp)
+    assert np.array_equal(v_dev.cpu().numpy(), vp)
+    buf.free()
+    with pytest.raises(ValueError):
+        buf.data_ptr()
+    buf.free()  # a second free is a no-op

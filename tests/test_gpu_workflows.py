@@ -1,4 +1,4 @@
-"""End-to-end workflows of BASELINE.json configs 3, 4 and 5 on the GPU.
+"""End-to-end workflows of BASELINE.json configs 1, 3, 4 and 5 on the GPU.
 
 Each test drives the product (PagedKvCache books + libdlmk kernels) and, in
 lockstep, a host mirror of the pools maintained by the CPU oracle from the same
@@ -136,14 +136,92 @@ def torch_mod(cuda):
     return torch
 
 
+def test_config1_16_layer_prefill_then_decode(oracle, torch_mod, cuda):
+    """BASELINE.json configs[0] as stated: Llama-3.2-1B KV (16 layers, 32 query
+    heads, 8 kv heads, head_dim 64, f32), one sequence whose blocks come from a
+    seeded-shuffled free list.  Each layer appends a 512-token prefill chunk,
+    then 64 decode steps append 1 token per layer and attend with scale 1/8.
+    Every layer of every step is compared with the oracle's attention() over
+    the host mirror (1e-5), even steps through the fused decode step and odd
+    steps as append + attention, and every layer's pools are bit-exact at the
+    end (src/forward/cpu.rs:1126-1151, :765-795)."""
+    from dlm_amd import KvCacheConfig, PagedKvCache, ops
+    from helpers import F32_ATOL, F32_RTOL
+    torch = torch_mod
+    L, Hq, Hkv, d, prefill, steps = 16, 32, 8, 64, 512, 64
+    banner(f"config-1 workflow: {L} layers, {prefill} prefill + {steps} decode steps")
+    nb, max_blocks = 64, 40
+    rng = np.random.default_rng(1)
+    cache = PagedKvCache.with_seeded_shuffle(KvCacheConfig(L, Hkv, d, BS), nb, seed=1)
+    kh = [(rng.standard_normal((nb, Hkv, d // 4, BS, 4))).astype(np.float32) for _ in range(L)]
+    vh = [(rng.standard_normal((nb, Hkv, d, BS))).astype(np.float32) for _ in range(L)]
+    kd = [to_dev(torch, a, cuda) for a in kh]
+    vd = [to_dev(torch, a, cuda) for a in vh]
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    dv = lambda a: to_dev(torch, a, cuda)
+    ws = ops.alloc_workspace(ops.attention_workspace_bytes(1, 1, Hq, d, max_blocks), cuda)
+
+    cache.append_tokens(0, prefill)
+    slots = cache.slot_mapping(0, 0, prefill)
+    for layer in range(L):
+        k = rng.standard_normal((prefill, Hkv, d)).astype(np.float32)
+        v = rng.standard_normal((prefill, Hkv, d)).astype(np.float32)
+        ops.kv_append(kd[layer], vd[layer], dv(k), dv(v), dv(slots), num_kv_heads=Hkv, head_dim=d)
+        oracle.paged_append(kh[layer], vh[layer], k, v, slots, Hkv, d, BS)
+    worst = 0.0
+    for step in range(steps):
+        cache.append_tokens(0, 1)
+        pos = prefill + step
+        slot = cache.slot_mapping(0, pos, 1)
+        tables, lens = cache.block_tables([0], max_blocks)
+        assert lens[0] == pos + 1
+        t_d, l_d = dv(tables), dv(lens)
+        qs, outs = [], []
+        for layer in range(L):
+            k = rng.standard_normal((1, Hkv, d)).astype(np.float32)
+            v = rng.standard_normal((1, Hkv, d)).astype(np.float32)
+            q = rng.standard_normal((1, 1, Hq, d)).astype(np.float32)
+            if step % 2 == 0:
+                out = ops.paged_decode_step(dv(q), dv(k), dv(v), kd[layer], vd[layer], t_d, l_d,
+                                            num_kv_heads=Hkv, scale=float(scale),
+                                            out_dtype=torch.float32, workspace=ws)
+            else:
+                ops.kv_append(kd[layer], vd[layer], dv(k), dv(v), dv(slot), num_kv_heads=Hkv,
+                              head_dim=d)
+                out = ops.paged_decode_attention(dv(q), kd[layer], vd[layer], t_d, l_d,
+                                                 num_kv_heads=Hkv, scale=float(scale),
+                                                 out_dtype=torch.float32, workspace=ws)
+            oracle.paged_append(kh[layer], vh[layer], k, v, slot, Hkv, d, BS)
+            qs.append(q)
+            outs.append(out)
+        torch.cuda.synchronize()
+        for layer in range(L):
+            ref = oracle.paged_attention(qs[layer], kh[layer], vh[layer], tables, lens, 1, Hq, Hkv,
+                                         d, BS, scale)
+            got = outs[layer].cpu().numpy()
+            assert_close(got, ref, F32_ATOL, F32_RTOL, f"config-1 step {step} layer {layer}")
+            worst = max(worst, float(np.abs(got - ref).max()))
+        if step % 16 == 0:
+            banner(f"config-1 step {step}: ctx {pos + 1}, worst abs err so far {worst:.2e}")
+    torch.cuda.synchronize()
+    for layer in range(L):
+        assert np.array_equal(kd[layer].cpu().numpy().view(np.uint32), kh[layer].view(np.uint32))
+        assert np.array_equal(vd[layer].cpu().numpy().view(np.uint32), vh[layer].view(np.uint32))
+    # The single table is shared by all 16 layers and came off the shuffled list.
+    table = cache.block_table(0)
+    assert len(table) == -(-(prefill + steps) // BS) and table != sorted(table)
+
+
 @pytest.mark.parametrize("full", [False, True])
 def test_config3_continuous_batching(oracle, torch_mod, cuda, full):
     """Decode sequences + chunked-prefill sequences share one free list; sequences
-    finish and are replaced; every step is checked against the oracle (reduced
-    sizes) or on a sampled subset (config-3 sizes: 48 decode at U[256, 8192] +
-    4 x 512-token chunks per step)."""
+    finish and are replaced; every step is checked against the oracle: all
+    sequences at reduced sizes; at config-3 sizes (48 decode at U[256, 8192] +
+    4 x 512-token chunks per step, all 200 steps) one sequence per step in
+    rotation plus a random second one, and every sequence on every 50th step.
+    Books are invariant after every step and the pools bit-exact at the end."""
     n_dec, lo, hi, n_pref, chunk, steps, pool = (
-        (48, 256, 8192, 4, 512, 24, 36000) if full else (12, 64, 1024, 2, 128, 30, 4000))
+        (48, 256, 8192, 4, 512, 200, 36000) if full else (12, 64, 1024, 2, 128, 30, 4000))
     banner(f"config-3 workflow full={full} steps={steps}")
     m = Mirror(torch_mod, cuda, oracle, pool, seed=3 + full)
     rng = np.random.default_rng(33 + full)
@@ -160,7 +238,12 @@ def test_config3_continuous_batching(oracle, torch_mod, cuda, full):
         work = [(s, 1) for s in decode] + [(s, min(chunk, r)) for s, r in prefill.items()]
         m.append(work)
         seqs = list(decode)
-        check = None if not full else rng.choice(len(seqs), 2, replace=False)
+        check = None
+        if full and step % 50 != 49:
+            check = sorted({step % len(seqs), int(rng.integers(len(seqs)))})
+        if full and step % 20 == 0:
+            banner(f"config-3 step {step}: {len(seqs)} decode sequences, "
+                   f"{m.cache.stats().used_blocks} blocks in use")
         m.attention(seqs, check=check, max_blocks=(hi + steps + 4 * chunk) // BS + 2)
         for s in list(prefill):
             prefill[s] -= min(chunk, prefill[s])
