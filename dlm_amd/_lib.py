@@ -77,6 +77,9 @@ SIGNATURES = {
     "dlmk_paged_decode_attention": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _i32,
                                            _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _vp,
                                            _sz]),
+    "dlmk_paged_decode_attention_noalloc": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp,
+                                                   _i32, _i32, _i32, _i32, _i32, _i32, _i32, _i64,
+                                                   _f32]),
     "dlmk_paged_decode_step": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _vp, _vp, _i32,
                                       _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _vp, _sz]),
     "dlmk_kv_append_quant": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _vp, _i64, _i32,

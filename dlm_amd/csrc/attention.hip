@@ -7,6 +7,8 @@
 // described in attention_kernels.h.
 #include "attention_kernels.h"
 
+#include <mutex>
+
 extern "C" {
 
 size_t dlmk_paged_attention_workspace_size(int num_seqs, int num_q_per_seq, int num_q_heads,
@@ -33,7 +35,8 @@ int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype
                          const void *v_new, const int32_t *block_tables, const int32_t *ctx_lens,
                          int num_seqs, int num_q_per_seq, int num_q_heads, int num_kv_heads,
                          int head_dim, int block_size, int max_blocks_per_seq, int64_t num_blocks,
-                         float scale, void *workspace, size_t workspace_bytes) {
+                         float scale, void *workspace, size_t workspace_bytes,
+                         bool exact_workspace = false) {
     if (num_seqs < 0 || num_q_per_seq <= 0 || num_q_heads <= 0 || num_kv_heads <= 0 ||
         head_dim <= 0 || max_blocks_per_seq <= 0 || num_blocks < 0)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: bad sizes", who);
@@ -80,21 +83,23 @@ int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype
     a.scale = scale;
     a.stream = (hipStream_t)stream;
     a.workspace = nullptr;
-    a.ws_o_bytes = 0;
+    a.ws_bytes = 0;
     const int64_t parts = parts_for(max_blocks_per_seq, kMinPartition);
     if (parts > 1) {
+        // The documented bound (dlmk_paged_attention_workspace_size) holds for
+        // every kernel; the launch checks the exact need of the partition size
+        // it picks (exact_workspace: only that check, for a fixed-size buffer).
         const size_t need = dlmk_paged_attention_workspace_size(
             num_seqs, num_q_per_seq, num_q_heads, head_dim, block_size, max_blocks_per_seq);
-        if (!workspace || workspace_bytes < need)
+        if (!workspace || (!exact_workspace && workspace_bytes < need))
             return dlmk::fail(DLMK_ERR_WORKSPACE,
                               "%s: workspace %zu bytes, need %zu", who,
                               workspace_bytes, need);
         if (reinterpret_cast<uintptr_t>(workspace) % 256 != 0)
             return dlmk::fail(DLMK_ERR_INVALID_ARG,
                               "%s: workspace not 256-byte aligned", who);
-        const int64_t rows = (int64_t)num_seqs * num_q_per_seq * num_q_heads;
         a.workspace = workspace;
-        a.ws_o_bytes = (rows * parts * head_dim * 4 + 255) / 256 * 256;
+        a.ws_bytes = workspace_bytes;
     }
     switch (dtype) {
         case DLMK_F32: return dlmk_attn::dispatch_f32(a, head_dim);
@@ -162,6 +167,80 @@ int dlmk_paged_decode_attention_quant(void *stream, void *out, int out_dtype, co
                                 num_seqs, num_q_per_seq, num_q_heads, num_kv_heads, head_dim,
                                 block_size, max_blocks_per_seq, num_blocks, scale, workspace,
                                 workspace_bytes);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Allocation-free attention (dlmk_paged_decode_attention_noalloc): the split-K
+// partials live in a file-scope device array instead of a caller workspace.
+// ---------------------------------------------------------------------------
+namespace {
+
+constexpr size_t kScratchBytes = DLMK_NOALLOC_SCRATCH_BYTES;
+
+}  // namespace
+
+// One copy per GPU the library runs on, held until the process ends.  In host
+// code `scratch` names a host-side stand-in: kernels only ever receive the
+// device address hipGetSymbolAddress returns (scratch_for_stream below).
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on the device that runs `stream` (the
+// current device for the null stream), looked up once per device with that
+// device current.
+int scratch_for_stream(hipStream_t stream, void **out) {
+    int cur = 0, dev = 0;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return dlmk::fail((int)e, "hipGetDevice: %s", hipGetErrorString(e));
+    dev = cur;
+    if (stream != nullptr) {
+        e = hipStreamGetDevice(stream, &dev);
+        if (e != hipSuccess)
+            return dlmk::fail((int)e, "hipStreamGetDevice: %s", hipGetErrorString(e));
+    }
+    if (dev < 0 || dev >= kMaxDevices)
+        return dlmk::fail(DLMK_ERR_UNSUPPORTED, "device %d beyond the scratch table", dev);
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess)
+            return dlmk::fail((int)e, "hipSetDevice(%d): %s", dev, hipGetErrorString(e));
+        void *p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (dev != cur) hipSetDevice(cur);
+        if (e != hipSuccess)
+            return dlmk::fail((int)e, "hipGetSymbolAddress(scratch): %s", hipGetErrorString(e));
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return DLMK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int dlmk_paged_decode_attention_noalloc(void *stream, void *out, int out_dtype, const void *q,
+                                        const void *k_pool, const void *v_pool, int dtype,
+                                        const int32_t *block_tables, const int32_t *ctx_lens,
+                                        int num_seqs, int num_q_per_seq, int num_q_heads,
+                                        int num_kv_heads, int head_dim, int block_size,
+                                        int max_blocks_per_seq, int64_t num_blocks, float scale) {
+    void *ws = nullptr;
+    const int rc = scratch_for_stream((hipStream_t)stream, &ws);
+    if (rc != DLMK_OK) return rc;
+    return paged_attention_impl("dlmk_paged_decode_attention_noalloc", stream, out, out_dtype, q,
+                                const_cast<void *>(k_pool), const_cast<void *>(v_pool), dtype,
+                                nullptr, nullptr, nullptr, nullptr, block_tables, ctx_lens, num_seqs,
+                                num_q_per_seq, num_q_heads, num_kv_heads, head_dim, block_size,
+                                max_blocks_per_seq, num_blocks, scale, ws, kScratchBytes,
+                                /*exact_workspace=*/true);
 }
 
 }  // extern "C"

@@ -56,8 +56,8 @@ struct Args {
     int B, NQ, Hq, Hkv, max_blocks;
     int64_t num_blocks;
     float scale;
-    void *workspace;
-    int64_t ws_o_bytes;
+    void *workspace;     // split-K partials, 256-byte aligned (may be NULL if never needed)
+    size_t ws_bytes;     // bytes available at workspace
     hipStream_t stream;
 };
 
@@ -1210,8 +1210,17 @@ int launch_pair(const Args &a, int partition, Launch launch) {
     const int max_parts = (int)parts_for(a.max_blocks, partition);
     float *ws_o = nullptr, *ws_ml = nullptr;
     if (max_parts > 1) {
+        // Workspace layout for this partition size: O partials
+        // [rows][max_parts][D] f32, then (m, l) pairs [rows][max_parts][2].
+        const int64_t rows = (int64_t)a.B * a.NQ * a.Hq;
+        const int64_t o_bytes = (rows * max_parts * D * 4 + 255) / 256 * 256;
+        const int64_t need = o_bytes + rows * max_parts * 2 * 4;
+        if (!a.workspace || (int64_t)a.ws_bytes < need)
+            return dlmk::fail(DLMK_ERR_WORKSPACE,
+                              "paged attention: split-K partials need %lld bytes, the workspace "
+                              "holds %zu", (long long)need, a.ws_bytes);
         ws_o = static_cast<float *>(a.workspace);
-        ws_ml = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + a.ws_o_bytes);
+        ws_ml = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + o_bytes);
     }
     launch(dim3((unsigned)(a.B * a.Hkv), (unsigned)max_parts), max_parts, ws_o, ws_ml);
     // Rows of up to kCombineBatch partitions: a wave per row (config 5

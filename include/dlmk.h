@@ -233,6 +233,24 @@ int dlmk_paged_decode_step(void *stream, void *out, int out_dtype, const void *q
                            int block_size, int max_blocks_per_seq, int64_t num_blocks, float scale,
                            void *workspace, size_t workspace_bytes);
 
+/* Allocation-free paged decode attention.  No counterpart in the reference:
+ * for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same
+ * arguments and results as dlmk_paged_decode_attention without the workspace:
+ * the split-K partials live in a library-owned device array of
+ * DLMK_NOALLOC_SCRATCH_BYTES per GPU (allocated with the code object, kept
+ * until the process ends).  Calls whose partials would exceed it return
+ * DLMK_ERR_WORKSPACE before launching anything.  Nothing in the array needs
+ * to start at zero; every call on one GPU shares it, so calls that overlap on
+ * one GPU (concurrent streams) race.  Never calls hipMalloc or hipFree. */
+#define DLMK_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int dlmk_paged_decode_attention_noalloc(void *stream, void *out, int out_dtype, const void *q,
+                                        const void *k_pool, const void *v_pool, int dtype,
+                                        const int32_t *block_tables, const int32_t *ctx_lens,
+                                        int num_seqs, int num_q_per_seq, int num_q_heads,
+                                        int num_kv_heads, int head_dim, int block_size,
+                                        int max_blocks_per_seq, int64_t num_blocks, float scale);
+
 /* Quantized KV pools (dlm's --kv-quant int8 / int4, KvLayerCache at
  * src/forward/cpu.rs:622-711).  Each token carries one f32 scale per pool over
  * its whole kv_dim (num_kv_heads * head_dim values): scale = max|x| / qmax
