@@ -621,7 +621,7 @@ def main():
         "roofline": {
             "bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
-            "kernel": "paged_attn_mfma_kernel" if w.dtype != "f32" else "paged_attn_valu_kernel",
+            "kernel": "paged_attn_mfma_kernel" if w.dtype != "f32" else "paged_attn_generic_kernel",
             "traffic_detail": traffic_note,
         },
     }

@@ -59,7 +59,7 @@ int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: bad out dtype %d", who,
                           out_dtype);
     if ((int64_t)num_seqs * num_kv_heads > 0x7fffffff ||
-        parts_for(max_blocks_per_seq, kMinPartition) > 65535 || num_seqs > 65535)
+        parts_for(max_blocks_per_seq, kMinPartition) > 65534 || num_seqs > 65535)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED, "%s: grid too large", who);
 
     Args a;
@@ -79,6 +79,7 @@ int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype
     a.Hq = num_q_heads;
     a.Hkv = num_kv_heads;
     a.max_blocks = max_blocks_per_seq;
+    a.D = head_dim;
     a.num_blocks = num_blocks;
     a.scale = scale;
     a.stream = (hipStream_t)stream;

@@ -1,16 +1,14 @@
-// Paged decode attention over f32 pools (VALU kernel): instantiates and launches
-// the kernels of attention_kernels.h for the supported head dims.
+// Paged decode attention over f32 pools (dlm's KV dtype, KvStore::Full,
+// src/forward/cpu.rs:641-650): the generic matrix-core kernel of
+// attention_kernels.h (v_mfma_f32_16x16x4_f32), any head dim that is a
+// multiple of 4 up to 256 and any GQA group / query count.
 #include "attention_kernels.h"
 
 namespace dlmk_attn {
 
 int dispatch_f32(const Args &a, int head_dim) {
-    const int gqa = a.Hq / a.Hkv;
-    switch (head_dim) {
-        case 64: return dispatch_valu<64>(a, gqa);
-        case 128: return dispatch_valu<128>(a, gqa);
-        default: return bad_dim(head_dim, "64, 128");
-    }
+    const int rc = dispatch_generic<float>(a);
+    return rc == -1 ? bad_dim(head_dim, "multiples of 4 up to 256") : rc;
 }
 
 }  // namespace dlmk_attn

@@ -56,6 +56,7 @@ struct Args {
     int B, NQ, Hq, Hkv, max_blocks;
     int64_t num_blocks;
     float scale;
+    int D;               // head dim
     void *workspace;     // split-K partials, 256-byte aligned (may be NULL if never needed)
     size_t ws_bytes;     // bytes available at workspace
     hipStream_t stream;
@@ -206,39 +207,6 @@ __device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][D],
                 ws_ml[2 * slot] = rowML[r][0];
                 ws_ml[2 * slot + 1] = L;
             }
-        }
-    }
-}
-
-// Fused decode step: the wave that owns block `blk` (logical block `lb`) of a
-// sequence writes the sequence's newest positions ctx - nq .. ctx - 1 that
-// fall in that block -- its kv head's K and V, the same bits dlmk_kv_append
-// would write.  Only this wave reads that tile in the launch.  The matrix-core
-// kernel takes the new values from k_new / v_new in registers and stores them
-// after its last tile load; the VALU kernel stores them before loading the
-// block, ordered by a wavefront-scope fence (a wave's global stores and later
-// loads of the same address are performed in program order).
-template <typename T, int D, bool NT>
-__device__ __forceinline__ void append_new_in_block(T *k_pool, T *v_pool, const T *k_new,
-                                                    const T *v_new, int64_t blk, int lb, int seq,
-                                                    int kvh, int num_kv_heads, int nq, int ctx,
-                                                    int lane) {
-    constexpr int X = 16 / sizeof(T);
-    constexpr int TILE = D * kBlock;
-    const int lo = max(ctx - nq, lb * kBlock), hi = min(ctx, lb * kBlock + kBlock);
-    const int64_t base = (blk * num_kv_heads + kvh) * TILE;
-    for (int e = lane; e < (hi - lo) * D; e += 64) {
-        const int p = lo + e / D, dim = e % D;
-        const int t = p - lb * kBlock, j = p - (ctx - nq);
-        const int64_t src = ((int64_t)(seq * nq + j) * num_kv_heads + kvh) * D + dim;
-        T *kd = &k_pool[base + (dim / X * kBlock + t) * X + dim % X];
-        T *vd = &v_pool[base + dim * kBlock + t];
-        if (NT) {
-            pool_store(kd, k_new[src]);
-            pool_store(vd, v_new[src]);
-        } else {
-            *kd = k_new[src];
-            *vd = v_new[src];
         }
     }
 }
@@ -822,212 +790,350 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
 }
 
 // ---------------------------------------------------------------------------
-// VALU partition kernel (f32 pools).
-//   K tile [d/4][16][4]: load i of lane l is chunk row l/16 + 4i of token l%16,
-//     so one lane holds a 4-chunk partial dot for one token and the score
-//     needs a 4-way cross-lane sum (xor 16, xor 32).
-//   V tile [d][16]: load i of lane l is 4 consecutive tokens of one dim, so a
-//     lane's accumulator is ROWS x (loads) floats summed across the 4 lanes
-//     sharing a dim.
+// Generic matrix-core partition kernel: any head dim hd <= DP (a multiple of
+// the pool's 16-byte chunk), any GQA group and query count (row groups of 16
+// query rows), f32 / f16 / bf16 pools.  The same tiling as
+// paged_attn_mfma_kernel with the geometry at run time: lanes of chunk rows
+// or dims past hd load an in-tile address (chunk row / dim 0) and meet zero Q
+// (scores) or are never stored (outputs), so any hd works without padding the
+// pools.  f32 pools use v_mfma_f32_16x16x4_f32: one 16-byte K chunk of a lane
+// is 4 steps of 4 dims, one 16-byte V load 4 tokens of one dim (4 steps).
 // ---------------------------------------------------------------------------
-template <int D, int GQA, int NQ, int NW, int P>
-__global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
-    void *__restrict__ out, int out_dtype, const float *__restrict__ q, float *__restrict__ k_pool,
-    float *__restrict__ v_pool, const float *__restrict__ k_new, const float *__restrict__ v_new,
-    const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
+template <typename T>
+struct GenOp;
+
+template <>
+struct GenOp<float> {
+    using KRaw = f32x4;  // 4 dims of one token (K) / 4 tokens of one dim (V)
+    using VRaw = f32x4;
+    using P4 = f32x4;    // P operand: 4 tokens of one row, kept in f32
+    static constexpr int X = 4;  // elements per 16-byte chunk
+    static __device__ __forceinline__ void qk(KRaw k, KRaw q, f32x4 &c0, f32x4 &c1) {
+        c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k[0], q[0], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k[1], q[1], c1, 0, 0, 0);
+        c0 = __builtin_amdgcn_mfma_f32_16x16x4f32(k[2], q[2], c0, 0, 0, 0);
+        c1 = __builtin_amdgcn_mfma_f32_16x16x4f32(k[3], q[3], c1, 0, 0, 0);
+    }
+    static __device__ __forceinline__ f32x4 pv(P4 p, VRaw v, f32x4 c) {
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(p[0], v[0], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(p[1], v[1], c, 0, 0, 0);
+        c = __builtin_amdgcn_mfma_f32_16x16x4f32(p[2], v[2], c, 0, 0, 0);
+        return __builtin_amdgcn_mfma_f32_16x16x4f32(p[3], v[3], c, 0, 0, 0);
+    }
+    static __device__ __forceinline__ float round_p(float p) { return p; }
+};
+
+template <typename E>
+struct GenOpHalf {  // f16 / bf16: one 16-byte chunk is one 16x16x32 step
+    using M = Mfma<E>;
+    using KRaw = typename M::x8;
+    using VRaw = typename M::x4;
+    using P4 = typename M::x4;
+    static constexpr int X = 8;
+    static __device__ __forceinline__ void qk(KRaw k, KRaw q, f32x4 &c0, f32x4 &) {
+        c0 = M::qk(k, q, c0);
+    }
+    static __device__ __forceinline__ f32x4 pv(P4 p, VRaw v, f32x4 c) { return M::pv(p, v, c); }
+    static __device__ __forceinline__ E round_p(float p) { return (E)p; }
+};
+template <>
+struct GenOp<_Float16> : GenOpHalf<_Float16> {};
+template <>
+struct GenOp<__bf16> : GenOpHalf<__bf16> {};
+
+// Runtime geometry of the generic kernel.
+struct GenGeom {
+    int hd;        // head dim (<= DP)
+    int gqa, nq;   // query heads per kv head, queries per sequence
+    int n_rg;      // row groups of 16 rows per (sequence, kv head)
+};
+
+template <typename T, int DP, int NW, int NB, int PD, bool FUSED>
+__global__ __launch_bounds__(NW * 64) void paged_attn_generic_kernel(
+    void *__restrict__ out, int out_dtype, const T *__restrict__ q, T *__restrict__ k_pool,
+    T *__restrict__ v_pool, const T *__restrict__ k_new, const T *__restrict__ v_new,
+    const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens, GenGeom geo,
     int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
     int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
-    constexpr int X = 4;                    // floats per 16-byte chunk
-    constexpr int CPL = D / X;              // chunks per token row
-    constexpr int KI = CPL / 4;             // 16-byte loads per lane per block (K and V alike)
-    constexpr int CPD = kBlock / X;         // V chunks per dim row of a tile
-    constexpr int ROWS = GQA * NQ;
-    constexpr int BPW = P / kBlock / NW;    // blocks per wave
-    constexpr int TILE = D * kBlock;
-    static_assert(CPL % 4 == 0 && BPW >= 1, "unsupported geometry");
+    using G = GenOp<T>;
+    using KRaw = typename G::KRaw;
+    using VRaw = typename G::VRaw;
+    constexpr int X = G::X;
+    constexpr int KL = DP / X / 4;   // 16-byte K (and Q) loads per lane per block
+    constexpr int VN = DP / 16;      // 16-dim PV steps (one V load each) per block
+    constexpr int P = NW * NB * kBlock;
+    static_assert(DP % (4 * X) == 0 && DP % 16 == 0, "unsupported padded head dim");
+    static_assert(NW >= 2, "new-token blocks must land on different waves");
 
-    __shared__ float p_lds[NW][BPW][ROWS][kBlock];
-    __shared__ float o_lds[NW][ROWS][D];
-    __shared__ float ml_lds[NW][ROWS][2];
+    __shared__ float o_lds[NW][16][DP];
+    __shared__ float ml_lds[NW][16][2];
 
-    // blockIdx.x = seq * num_kv_heads + kv head, blockIdx.y = partition: the
-    // dispatcher deals consecutive work-groups to the 8 XCDs round-robin, so
-    // with the (sequence, head) pair fastest every XCD gets the same mix of
-    // full and ragged partitions (partition-fastest would pin each XCD to one
-    // partition index, and late partitions exist only for long contexts).
-    // Partitions are dealt last index first: the high indices (long contexts
-    // only, mostly full) start early and the grid ends on partition 0, where
-    // the short sequences' small work-groups fill the drain (+1 point of HBM
-    // peak over first-index-first at the 8B shape).
-    const int part = gridDim.y - 1 - blockIdx.y, kvh = blockIdx.x % num_kv_heads,
-              seq = blockIdx.x / num_kv_heads;
-    const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int first_lb = part * (P / kBlock) + wave * BPW;
-    const int32_t *table = block_tables + (int64_t)seq * max_blocks;
-    // The table entries are read before the length (indices clamped into the
-    // row, not to the context), so the two reads overlap; entries past the
-    // context are masked below.
-    int32_t raw[BPW];
-#pragma unroll
-    for (int b = 0; b < BPW; ++b) raw[b] = table[min(first_lb + b, max_blocks - 1)];
-    const int len = ctx_lens[seq];
-    // Both reads are used here, so the compiler issues them together and
-    // cannot sink the table reads past the early exit below.
-#pragma unroll
-    for (int b = 0; b < BPW; ++b) asm volatile("" ::"s"(raw[b]), "s"(len));
-    const int ctx = min(len, max_blocks * kBlock);
+    const int hd = geo.hd, gqa = geo.gqa, nq = geo.nq;
+    const int64_t tile = (int64_t)hd * kBlock;  // elements per (block, kv head) tile
+    const int rg = blockIdx.x % geo.n_rg;
+    const int kvh = (blockIdx.x / geo.n_rg) % num_kv_heads;
+    const int seq = blockIdx.x / geo.n_rg / num_kv_heads;
+
+    if (FUSED && blockIdx.y == 0) {
+        // Fused decode step: the first grid row stores the new tokens (once
+        // per (sequence, kv head): row group 0); the partition work-groups
+        // substitute them from k_new / v_new.
+        if (rg == 0) {
+            const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+            for (int e = threadIdx.x; e < nq * hd; e += NW * 64) {
+                const int j = e / hd, dim = e % hd, p = ctx - nq + j;
+                if (p < 0) continue;
+                const int64_t blk = block_tables[(int64_t)seq * max_blocks + p / kBlock];
+                if (blk < 0 || blk >= num_blocks) continue;
+                const int t = p % kBlock;
+                const int64_t base = (blk * num_kv_heads + kvh) * tile;
+                const int64_t src = ((int64_t)(seq * nq + j) * num_kv_heads + kvh) * hd + dim;
+                pool_store(&k_pool[base + (dim / X * kBlock + t) * X + dim % X], k_new[src]);
+                pool_store(&v_pool[base + dim * kBlock + t], v_new[src]);
+            }
+        }
+        return;
+    }
+    // Partitions last index first (as paged_attn_mfma_kernel); with the
+    // append row at blockIdx.y 0 this still maps rows 1.. onto max_parts - 1 .. 0.
+    const int part = gridDim.y - 1 - blockIdx.y;
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
     const int nparts = parts_of(ctx, P);
     if (part >= nparts) return;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n = lane & 15;
     const int nblk_seq = (ctx + kBlock - 1) / kBlock;
+    const int32_t *table = block_tables + (int64_t)seq * max_blocks;
+    const int rows = gqa * nq;
+    const int rows_here = min(16, rows - rg * 16);
 
-    int64_t blk[BPW];
+    // Row n of this group: query j, head h.  Lanes past the group's rows load
+    // a valid row and are zeroed below.
+    const int r = rg * 16 + min(n, rows_here - 1);
+    const int qj = r / gqa, qh = kvh * gqa + r % gqa;
+    // This lane's chunk rows 4l + g (clamped into the tile past hd / X).
+    const int nchunk = hd / X;
+    int crow[KL];
 #pragma unroll
-    for (int b = 0; b < BPW; ++b) {
-        const int lb = first_lb + b;
-        int64_t id = lb < nblk_seq ? (int64_t)raw[b] : -1;
-        blk[b] = (id >= 0 && id < num_blocks) ? id : -1;
+    for (int l = 0; l < KL; ++l) crow[l] = 4 * l + g < nchunk ? 4 * l + g : 0;
+    KRaw qb[KL];
+    {
+        const KRaw *qp = reinterpret_cast<const KRaw *>(q + ((int64_t)(seq * nq + qj) * num_q_heads + qh) * hd);
+#pragma unroll
+        for (int l = 0; l < KL; ++l) qb[l] = qp[crow[l]];
     }
-    if (k_new != nullptr) {
+    const int limit = ctx - nq + qj + 1;
+
+    int lbs[NB];
+    int64_t blk[NB];
+    bool ok[NB];
+    int nvalid = 0;
+    int32_t raw[NB];
 #pragma unroll
-        for (int b = 0; b < BPW; ++b)
-            if (blk[b] >= 0 && holds_new(first_lb + b, ctx, NQ))
-                append_new_in_block<float, D, false>(k_pool, v_pool, k_new, v_new, blk[b], first_lb + b,
-                                              seq, kvh, num_kv_heads, NQ, ctx, lane);
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    for (int b = 0; b < NB; ++b) {
+        const int lb = part * (NW * NB) + wave_block(b, NB) * NW + wave;
+        raw[b] = table[max(min(lb, nblk_seq - 1), 0)];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+        const int lb = part * (NW * NB) + wave_block(b, NB) * NW + wave;
+        const int64_t id = lb < nblk_seq ? (int64_t)raw[b] : -1;
+        lbs[b] = lb;
+        ok[b] = id >= 0 && id < num_blocks;
+        blk[b] = id;
+        nvalid += ok[b];
     }
 
-    uint4 kb[BPW][KI], vb[BPW][KI];
+    float m = -INFINITY, lsum = 0.f;
+    f32x4 acc[VN];
 #pragma unroll
-    for (int b = 0; b < BPW; ++b) {
-        if (blk[b] >= 0) {
-            const int64_t base = (blk[b] * num_kv_heads + kvh) * TILE;
-            const uint4 *kp = reinterpret_cast<const uint4 *>(k_pool + base);
-            const uint4 *vp = reinterpret_cast<const uint4 *>(v_pool + base);
+    for (int k = 0; k < VN; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // Fused step: this wave's block holding new tokens, if any (see
+    // paged_attn_mfma_kernel), and the new tokens' chunks in registers.
+    int bnew = -1;
+    if constexpr (FUSED) {
 #pragma unroll
-            for (int i = 0; i < KI; ++i) kb[b][i] = kp[64 * i + lane];
+        for (int b = 0; b < NB; ++b)
+            if (ok[b] && holds_new(lbs[b], ctx, nq)) bnew = b;
+    }
+    bnew = __builtin_amdgcn_readfirstlane(bnew);
+    const int lb_new = part * (NW * NB) + wave_block(max(bnew, 0), NB) * NW + wave;
+    const int first_new = ctx - nq;
+    const int jk = lb_new * kBlock + n - first_new;
+    const bool k_is_new = jk >= 0 && jk < nq;
+    KRaw knew[KL];
+    VRaw vnew[VN];
+    int vdim[VN];
 #pragma unroll
-            for (int i = 0; i < KI; ++i) vb[b][i] = vp[64 * i + lane];
-        } else {
+    for (int k = 0; k < VN; ++k) vdim[k] = 16 * k + n < hd ? 16 * k + n : 0;
+    if (FUSED && bnew >= 0) {
+        const KRaw *kr = reinterpret_cast<const KRaw *>(
+            k_new + ((int64_t)(seq * nq + min(max(jk, 0), nq - 1)) * num_kv_heads + kvh) * hd);
 #pragma unroll
-            for (int i = 0; i < KI; ++i) kb[b][i] = vb[b][i] = make_uint4(0, 0, 0, 0);
+        for (int l = 0; l < KL; ++l) knew[l] = kr[crow[l]];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int jv = min(max(lb_new * kBlock + 4 * g + e - first_new, 0), nq - 1);
+            const T *vr = v_new + ((int64_t)(seq * nq + jv) * num_kv_heads + kvh) * hd;
+#pragma unroll
+            for (int k = 0; k < VN; ++k) vnew[k][e] = vr[vdim[k]];
         }
     }
 
-    uint4 qr[ROWS][KI];
+    if (nvalid > 0) {
+        int64_t first = 0;
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        const int j = r / GQA, h = kvh * GQA + r % GQA;
-        const uint4 *qp = reinterpret_cast<const uint4 *>(
-            q + ((int64_t)(seq * NQ + j) * num_q_heads + h) * D);
+        for (int b = NB - 1; b >= 0; --b)
+            if (ok[b]) first = blk[b];
 #pragma unroll
-        for (int i = 0; i < KI; ++i) qr[r][i] = qp[(lane >> 4) + 4 * i];
-    }
+        for (int b = 0; b < NB; ++b)
+            if (!ok[b]) blk[b] = first;
 
-    const int tok = lane & 15;
-    float s[BPW][ROWS];
+        KRaw kb[NB][KL];
+        VRaw vb[NB][VN];
+        auto issue = [&](int t) {
+            if (t < NB) {
+                const KRaw *kt = reinterpret_cast<const KRaw *>(k_pool + (blk[t] * num_kv_heads + kvh) * tile);
 #pragma unroll
-    for (int b = 0; b < BPW; ++b)
+                for (int l = 0; l < KL; ++l) kb[t][l] = stream_load(kt + crow[l] * kBlock + n);
+            } else if (t < 2 * NB) {
+                const VRaw *vt = reinterpret_cast<const VRaw *>(v_pool + (blk[t - NB] * num_kv_heads + kvh) * tile);
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            float acc = 0.f;
-#pragma unroll
-            for (int i = 0; i < KI; ++i) {
-                acc = fmaf(__uint_as_float(qr[r][i].x), __uint_as_float(kb[b][i].x), acc);
-                acc = fmaf(__uint_as_float(qr[r][i].y), __uint_as_float(kb[b][i].y), acc);
-                acc = fmaf(__uint_as_float(qr[r][i].z), __uint_as_float(kb[b][i].z), acc);
-                acc = fmaf(__uint_as_float(qr[r][i].w), __uint_as_float(kb[b][i].w), acc);
+                for (int k = 0; k < VN; ++k) vb[t - NB][k] = stream_load(vt + vdim[k] * 4 + g);
             }
-            acc += __shfl_xor(acc, 16);
-            acc += __shfl_xor(acc, 32);
-            s[b][r] = acc;
+        };
+#pragma unroll
+        for (int t = 0; t < PD; ++t) issue(t);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int l = 0; l < KL; ++l) qb[l] = n < rows_here && 4 * l + g < nchunk ? qb[l] : KRaw{};
+
+        float s[NB][4];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+            issue(b + PD);
+            __builtin_amdgcn_sched_barrier(0);
+            if (FUSED && b == bnew) {
+#pragma unroll
+                for (int l = 0; l < KL; ++l) kb[b][l] = k_is_new ? knew[l] : kb[b][l];
+            }
+            f32x4 c = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int l = 0; l < KL; ++l) {
+                if (l & 1)
+                    G::qk(kb[b][l], qb[l], c1, c);
+                else
+                    G::qk(kb[b][l], qb[l], c, c1);
+            }
+            c += c1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pos = lbs[b] * kBlock + 4 * g + j;
+                s[b][j] = (ok[b] && pos < limit) ? c[j] * scale_log2 : -INFINITY;
+            }
+            __builtin_amdgcn_sched_barrier(0);
         }
-
-    float m[ROWS], l[ROWS];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r) {
-        const int limit = ctx - NQ + r / GQA + 1;
-        float mx = -INFINITY;
+        for (int b = 0; b < NB; ++b)
 #pragma unroll
-        for (int b = 0; b < BPW; ++b) {
-            const int pos = (first_lb + b) * kBlock + tok;
-            const bool vis = blk[b] >= 0 && pos < limit;
-            s[b][r] = vis ? s[b][r] * scale_log2 : -INFINITY;
-            mx = fmaxf(mx, s[b][r]);
-        }
-        mx = xor_max<16>(mx);
-        float sum = 0.f;
-#pragma unroll
-        for (int b = 0; b < BPW; ++b) {
-            const float p = mx == -INFINITY ? 0.f : exp2f(s[b][r] - mx);
-            s[b][r] = p;
-            sum += p;
-        }
-        m[r] = mx;
-        l[r] = xor_sum<16>(sum);
-    }
+            for (int j = 0; j < 4; ++j) m = fmaxf(m, s[b][j]);
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
 
 #pragma unroll
-    for (int b = 0; b < BPW; ++b)
+        for (int b = 0; b < NB; ++b) {
+            issue(NB + b + PD);
+            __builtin_amdgcn_sched_barrier(0);
+            const int valid = __builtin_amdgcn_readfirstlane(ok[b] ? ctx - lbs[b] * kBlock : 0);
+            typename G::P4 pa;
 #pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-            if ((r & 3) == (lane >> 4)) p_lds[wave][b][r][tok] = s[b][r];
-    __syncthreads();
-
-    const int tg = lane % CPD;
-    float acc[ROWS][KI];
+            for (int j = 0; j < 4; ++j) {
+                const float p = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[b][j] - m);
+                pa[j] = G::round_p(p);
+                lsum += (float)pa[j];
+            }
+            VRaw vo[VN];
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r)
+            for (int k = 0; k < VN; ++k) vo[k] = vb[b][k];
+            if (FUSED && b == bnew) {
 #pragma unroll
-        for (int i = 0; i < KI; ++i) acc[r][i] = 0.f;
-
+                for (int e = 0; e < 4; ++e) {
+                    const int jv = lb_new * kBlock + 4 * g + e - first_new;
+                    if (jv >= 0 && jv < nq) {
 #pragma unroll
-    for (int b = 0; b < BPW; ++b) {
-        if (blk[b] < 0) continue;
-        float pr[ROWS][X];
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-            for (int e = 0; e < X; ++e) pr[r][e] = p_lds[wave][b][r][tg * X + e];
-        const int valid = ctx - (first_lb + b) * kBlock;
-#pragma unroll
-        for (int i = 0; i < KI; ++i) {
-            float v[X] = {__uint_as_float(vb[b][i].x), __uint_as_float(vb[b][i].y),
-                          __uint_as_float(vb[b][i].z), __uint_as_float(vb[b][i].w)};
+                        for (int k = 0; k < VN; ++k) vo[k][e] = vnew[k][e];
+                    }
+                }
+            }
+            // V past the context can hold NaN, and 0 * NaN is NaN: zero it.
             if (valid < kBlock) {
 #pragma unroll
-                for (int e = 0; e < X; ++e)
-                    if (tg * X + e >= valid) v[e] = 0.f;
+                for (int k = 0; k < VN; ++k)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        vo[k][e] = 4 * g + e < valid ? vo[k][e] : (T)0.f;
             }
 #pragma unroll
-            for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-                for (int e = 0; e < X; ++e) acc[r][i] = fmaf(pr[r][e], v[e], acc[r][i]);
+            for (int k = 0; k < VN; ++k) acc[k] = G::pv(pa, vo[k], acc[k]);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
 
+    // acc[k][j] = O[row 4g + j][dim 16k + n].
 #pragma unroll
-    for (int r = 0; r < ROWS; ++r)
+    for (int k = 0; k < VN; ++k)
 #pragma unroll
-        for (int i = 0; i < KI; ++i) acc[r][i] = xor_sum<CPD>(acc[r][i]);
-
-    if (tg == 0) {
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r)
-#pragma unroll
-            for (int i = 0; i < KI; ++i) o_lds[wave][r][(64 * i + lane) / CPD] = acc[r][i];
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int r = 0; r < ROWS; ++r) {
-            ml_lds[wave][r][0] = m[r];
-            ml_lds[wave][r][1] = l[r];
-        }
+        for (int j = 0; j < 4; ++j) o_lds[wave][4 * g + j][16 * k + n] = acc[k][j];
+    if (g == 0) {
+        ml_lds[wave][n][0] = m;
+        ml_lds[wave][n][1] = lsum;
     }
     __syncthreads();
-    merge_waves<ROWS, D, NW, GQA, NQ>(o_lds, ml_lds, out, out_dtype, seq, kvh, part, nparts,
-                                      num_q_heads, max_parts, ws_o, ws_ml);
+
+    // Merge the waves (as merge_waves, with the geometry at run time).
+    __shared__ float fac[16][NW];
+    __shared__ float rowML[16][2];
+    if (threadIdx.x < 16) {
+        const int rr = threadIdx.x;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) M = fmaxf(M, ml_lds[w][rr][0]);
+        float L = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) {
+            const float mw = ml_lds[w][rr][0];
+            const float f = (M == -INFINITY || mw == -INFINITY) ? 0.f : exp2f(mw - M);
+            fac[rr][w] = f;
+            L = fmaf(f, ml_lds[w][rr][1], L);
+        }
+        rowML[rr][0] = M;
+        rowML[rr][1] = L;
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < rows_here * hd; idx += NW * 64) {
+        const int rr = idx / hd, d = idx - rr * hd;
+        float O = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) O = fmaf(fac[rr][w], o_lds[w][rr][d], O);
+        const float L = rowML[rr][1];
+        const int gr = rg * 16 + rr, j = gr / gqa, h = kvh * gqa + gr % gqa;
+        const int64_t row = (int64_t)(seq * nq + j) * num_q_heads + h;
+        if (nparts == 1) {
+            store_out(out, out_dtype, row * hd + d, L > 0.f ? O / L : 0.f);
+        } else {
+            const int64_t slot = row * max_parts + part;
+            ws_o[slot * hd + d] = O;
+            if (d == 0) {
+                ws_ml[2 * slot] = rowML[rr][0];
+                ws_ml[2 * slot + 1] = L;
+            }
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1038,12 +1144,13 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_valu_kernel(
 constexpr int kCombineWaves = 4;
 constexpr int kCombineBatch = 8;
 
-template <int D>
+// DPL dims per lane: head dim D <= 64 * DPL (dims past D are read clamped and
+// never stored).
+template <int DPL>
 __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wave_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
     const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
-    int max_blocks, int partition, int max_parts) {
-    constexpr int DPL = D / 64;  // dims per lane
+    int max_blocks, int partition, int max_parts, int D) {
     constexpr int B = kCombineBatch;  // partitions loaded per batch
     // One wave per (sequence, query row), kCombineWaves rows per work-group:
     // the wave folds all of the row's partitions itself (online rescale), so
@@ -1064,7 +1171,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wave_ke
             mb[i] = ml[2 * p];
             lb[i] = ml[2 * p + 1];
 #pragma unroll
-            for (int k = 0; k < DPL; ++k) ob[i][k] = o[(int64_t)p * D + lane + 64 * k];
+            for (int k = 0; k < DPL; ++k) ob[i][k] = o[(int64_t)p * D + min(lane + 64 * k, D - 1)];
         }
     };
     // The first batch is read before the context length is known (every
@@ -1097,22 +1204,21 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wave_ke
     }
 #pragma unroll
     for (int k = 0; k < DPL; ++k)
-        store_out(out, out_dtype, row * D + lane + 64 * k, L > 0.f ? O[k] / L : 0.f);
+        if (lane + 64 * k < D) store_out(out, out_dtype, row * D + lane + 64 * k, L > 0.f ? O[k] / L : 0.f);
 }
 
 // Rows of more than kCombineBatch partitions: one work-group of
 // kCombineWaves waves per (query row, sequence).  Wave w loads its first
 // partition (w) before the context length arrives, folds w + W, ... in
 // batches with an online rescale, and the waves merge once in LDS.
-template <int D>
+template <int DPL>
 __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
     const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
-    int max_blocks, int partition, int max_parts) {
+    int max_blocks, int partition, int max_parts, int D) {
     constexpr int W = kCombineWaves;
-    constexpr int DPL = D / 64;  // dims per lane
     __shared__ float wml[W][2];
-    __shared__ float so[W][D + 1];
+    __shared__ float so[W][64 * DPL + 1];
     const int seq = blockIdx.y;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int64_t row = (int64_t)seq * rows_per_seq + blockIdx.x;
@@ -1132,7 +1238,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kern
         m0 = ml[2 * wave];
         l0 = ml[2 * wave + 1];
 #pragma unroll
-        for (int k = 0; k < DPL; ++k) o0[k] = o[(int64_t)wave * D + lane + 64 * k];
+        for (int k = 0; k < DPL; ++k) o0[k] = o[(int64_t)wave * D + min(lane + 64 * k, D - 1)];
     }
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
     const int nparts = parts_of(ctx, partition);
@@ -1155,7 +1261,7 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kern
             mb[i] = ml[2 * p];
             lb[i] = ml[2 * p + 1];
 #pragma unroll
-            for (int k = 0; k < DPL; ++k) ob[i][k] = o[(int64_t)p * D + lane + 64 * k];
+            for (int k = 0; k < DPL; ++k) ob[i][k] = o[(int64_t)p * D + min(lane + 64 * k, D - 1)];
         }
 #pragma unroll
         for (int i = 0; i < B; ++i) {
@@ -1203,17 +1309,39 @@ inline int64_t parts_for(int max_blocks, int partition) {
     return tokens > partition ? dlmk::ceil_div(tokens, partition) : 1;
 }
 
-// Launches the partition kernel through `launch(grid, max_parts, ws_o, ws_ml)`,
-// then the combine kernel when a sequence can span several partitions.
-template <int D, typename Launch>
-int launch_pair(const Args &a, int partition, Launch launch) {
+// Combine launch for DPL dims per lane (head dim <= 64 * DPL).
+template <int DPL>
+void launch_combine(const Args &a, int partition, int max_parts, float *ws_o, float *ws_ml) {
+    // Rows of up to kCombineBatch partitions: a wave per row (config 5
+    // 64.9 -> 66.2%); longer rows: a work-group per row, whose four waves
+    // share the row's partitions (the wave-per-row kernel was 0.8 points
+    // slower at config 4's 32 partitions and 2.9 us slower in the decode
+    // block's 32).
+    if (max_parts > kCombineBatch)
+        hipLaunchKernelGGL(paged_attn_combine_wg_kernel<DPL>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
+                           dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
+                           a.NQ * a.Hq, a.max_blocks, partition, max_parts, a.D);
+    else
+        hipLaunchKernelGGL(paged_attn_combine_wave_kernel<DPL>,
+                           dim3((unsigned)((a.NQ * a.Hq + kCombineWaves - 1) / kCombineWaves), (unsigned)a.B),
+                           dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
+                           a.NQ * a.Hq, a.max_blocks, partition, max_parts, a.D);
+}
+
+// Launches the partition kernel through `launch(grid, max_parts, ws_o, ws_ml)`
+// over grid_x x max_parts work-groups, then the combine kernel when a
+// sequence can span several partitions.
+template <typename Launch>
+int launch_pair(const Args &a, int partition, int64_t grid_x, Launch launch) {
     const int max_parts = (int)parts_for(a.max_blocks, partition);
     float *ws_o = nullptr, *ws_ml = nullptr;
+    if (grid_x > 0x7fffffff)
+        return dlmk::fail(DLMK_ERR_UNSUPPORTED, "paged attention: grid too large");
     if (max_parts > 1) {
         // Workspace layout for this partition size: O partials
         // [rows][max_parts][D] f32, then (m, l) pairs [rows][max_parts][2].
         const int64_t rows = (int64_t)a.B * a.NQ * a.Hq;
-        const int64_t o_bytes = (rows * max_parts * D * 4 + 255) / 256 * 256;
+        const int64_t o_bytes = (rows * max_parts * a.D * 4 + 255) / 256 * 256;
         const int64_t need = o_bytes + rows * max_parts * 2 * 4;
         if (!a.workspace || (int64_t)a.ws_bytes < need)
             return dlmk::fail(DLMK_ERR_WORKSPACE,
@@ -1222,21 +1350,15 @@ int launch_pair(const Args &a, int partition, Launch launch) {
         ws_o = static_cast<float *>(a.workspace);
         ws_ml = reinterpret_cast<float *>(static_cast<char *>(a.workspace) + o_bytes);
     }
-    launch(dim3((unsigned)(a.B * a.Hkv), (unsigned)max_parts), max_parts, ws_o, ws_ml);
-    // Rows of up to kCombineBatch partitions: a wave per row (config 5
-    // 64.9 -> 66.2%); longer rows: a work-group per row, whose four waves
-    // share the row's partitions (the wave-per-row kernel was 0.8 points
-    // slower at config 4's 32 partitions and 2.9 us slower in the decode
-    // block's 32).
-    if (max_parts > kCombineBatch)
-        hipLaunchKernelGGL(paged_attn_combine_wg_kernel<D>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
-                           dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
-                           a.NQ * a.Hq, a.max_blocks, partition, max_parts);
-    else if (max_parts > 1)
-        hipLaunchKernelGGL(paged_attn_combine_wave_kernel<D>,
-                           dim3((unsigned)((a.NQ * a.Hq + kCombineWaves - 1) / kCombineWaves), (unsigned)a.B),
-                           dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
-                           a.NQ * a.Hq, a.max_blocks, partition, max_parts);
+    launch(dim3((unsigned)grid_x, (unsigned)max_parts), max_parts, ws_o, ws_ml);
+    if (max_parts > 1) {
+        switch ((a.D + 63) / 64) {
+            case 1: launch_combine<1>(a, partition, max_parts, ws_o, ws_ml); break;
+            case 2: launch_combine<2>(a, partition, max_parts, ws_o, ws_ml); break;
+            case 3: launch_combine<3>(a, partition, max_parts, ws_o, ws_ml); break;
+            default: launch_combine<4>(a, partition, max_parts, ws_o, ws_ml); break;
+        }
+    }
     hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return dlmk::fail((int)e, "paged attention launch: %s", hipGetErrorString(e));
@@ -1250,7 +1372,8 @@ int launch_mfma(const Args &a) {
     constexpr int PD = C::kScaled ? DLMK_MFMA_PDQ : DLMK_MFMA_PD;
     static_assert(NW * NB * kBlock >= kMinPartition, "partition below the workspace bound");
     using QT = typename C::QT;
-    return launch_pair<D>(a, NW * NB * kBlock, [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
+    return launch_pair(a, NW * NB * kBlock, (int64_t)a.B * a.Hkv,
+                       [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
         // Fused decode step: one more grid row of append work-groups.
         if (!C::kScaled && a.k_new != nullptr) grid.y += 1;
         hipLaunchKernelGGL((paged_attn_mfma_kernel<C, D, GQA, NQ, NW, NB, PD>), grid, dim3(NW * 64), 0,
@@ -1262,36 +1385,93 @@ int launch_mfma(const Args &a) {
     });
 }
 
-// 256-token partitions when that grid fills the chip; otherwise smaller
-// partitions, as large as still give kValuMinGrid work-groups (a single
-// decoding sequence, as in dlmk_decode_block_paged, has num_kv_heads x
-// ctx / 256 work-groups: 64 at the 8B shape and ctx 2048).  Measured at the
-// decode block's shape (ctx 2048: 128 work-groups with 128-token partitions)
-// 128-token beat 64-token partitions by 1.1 us a layer; at config 1's
-// (ctx 640: 40 of them) 64-token ones won by 0.4 us.
-constexpr int64_t kValuSmallGrid = 1024;  // work-groups
-constexpr int64_t kValuMinGrid = 128;
-
-template <int D, int GQA, int NQ, int NW, int P>
-int launch_valu_p(const Args &a) {
-    static_assert(P >= kMinPartition, "partition below the workspace bound");
-    return launch_pair<D>(a, P, [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
-        hipLaunchKernelGGL((paged_attn_valu_kernel<D, GQA, NQ, NW, P>), grid, dim3(NW * 64), 0, a.stream,
-                           a.out, a.out_dtype, static_cast<const float *>(a.q),
-                           static_cast<float *>(a.k_pool), static_cast<float *>(a.v_pool),
-                           static_cast<const float *>(a.k_new), static_cast<const float *>(a.v_new),
-                           a.tables, a.ctx_lens, a.Hq, a.Hkv, a.max_blocks, a.num_blocks,
+// Generic kernel, NB blocks per wave (FUSED: with the fused step's append).
+template <typename T, int DP, int NB, bool FUSED>
+int launch_generic_nb(const Args &a) {
+    constexpr int NW = 4, PD = 2;
+    static_assert(NW * NB * kBlock >= kMinPartition, "partition below the workspace bound");
+    const int gqa = a.Hq / a.Hkv;
+    const GenGeom geo{a.D, gqa, a.NQ, (gqa * a.NQ + 15) / 16};
+    return launch_pair(a, NW * NB * kBlock, (int64_t)a.B * a.Hkv * geo.n_rg,
+                       [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
+        if (FUSED) grid.y += 1;  // the fused step's append row
+        hipLaunchKernelGGL((paged_attn_generic_kernel<T, DP, NW, NB, PD, FUSED>), grid, dim3(NW * 64), 0,
+                           a.stream, a.out, a.out_dtype, static_cast<const T *>(a.q),
+                           static_cast<T *>(a.k_pool), static_cast<T *>(a.v_pool),
+                           static_cast<const T *>(a.k_new), static_cast<const T *>(a.v_new),
+                           a.tables, a.ctx_lens, geo, a.Hq, a.Hkv, a.max_blocks, a.num_blocks,
                            a.scale * kLog2e, max_parts, ws_o, ws_ml);
     });
 }
 
-template <int D, int GQA, int NQ>
-int launch_valu(const Args &a) {
-    constexpr int NW = GQA * NQ <= 4 ? 4 : 8;
-    const auto grid = [&](int p) { return (int64_t)a.B * a.Hkv * parts_for(a.max_blocks, p); };
-    if (grid(256) >= kValuSmallGrid) return launch_valu_p<D, GQA, NQ, NW, 256>(a);
-    if (grid(128) >= kValuMinGrid) return launch_valu_p<D, GQA, NQ, NW, 128>(a);
-    return launch_valu_p<D, GQA, NQ, NW, NW * kBlock>(a);
+// Partition size by grid: the large partitions when that grid fills the chip
+// (kGenFullGrid work-groups); otherwise 128-token partitions while they still
+// give kGenMinGrid work-groups (a single decoding sequence, as in
+// dlmk_decode_block_paged, has num_kv_heads x ctx / 128 of them: 128 at the
+// 8B shape and ctx 2048), else 64-token ones.
+constexpr int64_t kGenFullGrid = 1024;
+constexpr int64_t kGenMinGrid = 128;
+
+template <typename T, int DP, bool FUSED>
+int launch_generic_f(const Args &a) {
+    // Large partitions: 256 tokens of f32 (NB 4) or 1024 of f16 / bf16 (NB
+    // 16).  The fused step picks the same shape as the plain launch, so its
+    // output is the same bits as append + attention.
+    constexpr int NB_BIG = sizeof(T) == 4 ? 4 : 16;
+    const int64_t rgs = (a.Hq / a.Hkv * a.NQ + 15) / 16;
+    const auto grid = [&](int p) { return (int64_t)a.B * a.Hkv * rgs * parts_for(a.max_blocks, p); };
+#ifdef DLMK_GEN_FORCE_NB
+    if (DLMK_GEN_FORCE_NB == 1) return launch_generic_nb<T, DP, 1, FUSED>(a);
+    if (DLMK_GEN_FORCE_NB == 2) return launch_generic_nb<T, DP, 2, FUSED>(a);
+#endif
+    if (grid(4 * NB_BIG * kBlock) >= kGenFullGrid) return launch_generic_nb<T, DP, NB_BIG, FUSED>(a);
+    if (grid(4 * 2 * kBlock) >= kGenMinGrid) return launch_generic_nb<T, DP, 2, FUSED>(a);
+    return launch_generic_nb<T, DP, 1, FUSED>(a);
+}
+
+template <typename T, int DP>
+int launch_generic(const Args &a) {
+    return a.k_new != nullptr ? launch_generic_f<T, DP, true>(a) : launch_generic_f<T, DP, false>(a);
+}
+
+// Padded head dims of the generic kernel: hd is rounded up to the next one.
+// f32 pools: multiples of 4 up to 256; f16 / bf16: multiples of 8 up to 256.
+template <typename T>
+int dispatch_generic(const Args &a) {
+    const int hd = a.D;
+    if constexpr (sizeof(T) == 4) {
+        if (hd % 4 != 0 || hd > 256) return -1;
+        if (hd <= 16) return launch_generic<T, 16>(a);
+        if (hd <= 32) return launch_generic<T, 32>(a);
+        if (hd <= 48) return launch_generic<T, 48>(a);
+        if (hd <= 64) return launch_generic<T, 64>(a);
+        if (hd <= 80) return launch_generic<T, 80>(a);
+        if (hd <= 96) return launch_generic<T, 96>(a);
+        if (hd <= 128) return launch_generic<T, 128>(a);
+        if (hd <= 192) return launch_generic<T, 192>(a);
+        return launch_generic<T, 256>(a);
+    } else {
+        if (hd % 8 != 0 || hd > 256) return -1;
+        if (hd <= 32) return launch_generic<T, 32>(a);
+        if (hd <= 64) return launch_generic<T, 64>(a);
+        if (hd <= 96) return launch_generic<T, 96>(a);
+        if (hd <= 128) return launch_generic<T, 128>(a);
+        if (hd <= 160) return launch_generic<T, 160>(a);
+        if (hd <= 192) return launch_generic<T, 192>(a);
+        return launch_generic<T, 256>(a);
+    }
+}
+
+// (GQA group, queries) pairs with an instantiated paged_attn_mfma_kernel.
+inline bool mfma_rows(int gqa, int nq) {
+    switch (gqa * 16 + nq) {
+        case 1 * 16 + 1: case 1 * 16 + 2: case 1 * 16 + 4:
+        case 2 * 16 + 1: case 2 * 16 + 2: case 2 * 16 + 4:
+        case 4 * 16 + 1: case 4 * 16 + 2: case 4 * 16 + 4:
+        case 8 * 16 + 1: case 8 * 16 + 2:
+        case 16 * 16 + 1: return true;
+        default: return false;
+    }
 }
 
 inline int unsupported_rows(int gqa, int nq) {
@@ -1315,22 +1495,6 @@ int dispatch_mfma(const Args &a, int gqa) {
         case 8 * 16 + 1: return launch_mfma<C, D, 8, 1>(a);
         case 8 * 16 + 2: return launch_mfma<C, D, 8, 2>(a);
         case 16 * 16 + 1: return launch_mfma<C, D, 16, 1>(a);
-        default: return unsupported_rows(gqa, a.NQ);
-    }
-}
-
-template <int D>
-int dispatch_valu(const Args &a, int gqa) {
-    switch (gqa * 16 + a.NQ) {
-        case 1 * 16 + 1: return launch_valu<D, 1, 1>(a);
-        case 1 * 16 + 2: return launch_valu<D, 1, 2>(a);
-        case 1 * 16 + 4: return launch_valu<D, 1, 4>(a);
-        case 2 * 16 + 1: return launch_valu<D, 2, 1>(a);
-        case 2 * 16 + 2: return launch_valu<D, 2, 2>(a);
-        case 2 * 16 + 4: return launch_valu<D, 2, 4>(a);
-        case 4 * 16 + 1: return launch_valu<D, 4, 1>(a);
-        case 4 * 16 + 2: return launch_valu<D, 4, 2>(a);
-        case 8 * 16 + 1: return launch_valu<D, 8, 1>(a);
         default: return unsupported_rows(gqa, a.NQ);
     }
 }

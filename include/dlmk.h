@@ -208,7 +208,10 @@ size_t dlmk_paged_attention_workspace_size(int num_seqs, int num_q_per_seq, int 
  * length above max_blocks_per_seq * block_size is clamped to it.
  * Contexts are split into fixed partitions processed in parallel and merged by
  * log-sum-exp in a second pass; workspace holds the partials
- * (>= dlmk_paged_attention_workspace_size bytes, 256-byte aligned). */
+ * (>= dlmk_paged_attention_workspace_size bytes, 256-byte aligned).
+ * Geometry: block_size 16; any num_q_heads / num_kv_heads group and
+ * num_q_per_seq; head_dim a multiple of 4 (f32) or 8 (f16, bf16) up to 256;
+ * otherwise DLMK_ERR_UNSUPPORTED. */
 int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const void *q,
                                 const void *k_pool, const void *v_pool, int dtype,
                                 const int32_t *block_tables, const int32_t *ctx_lens,
@@ -341,8 +344,8 @@ int dlmk_swap_in(void *stream, void *k_pool, void *v_pool, const void *host_buf,
  * host-computed rope_inv_freqs (src/forward/cpu.rs:1057-1092).  Weight rows
  * are read 16 bytes at a time: hidden_size, q_dim, inter and (int4/int8) the
  * group size must be multiples of 4 (f32), 8 (bf16, f16), 32 (int4) or 16
- * (int8) elements, else DLMK_ERR_UNSUPPORTED; head_dim must be 64 or 128 and
- * num_heads / num_kv_heads 1, 2, 4 or 8 (the f32 paged attention kernels).
+ * (int8) elements, else DLMK_ERR_UNSUPPORTED; head_dim is even, a multiple of
+ * 4 and at most 256, with any GQA group (the f32 paged attention kernel).
  * Returns 0 or an error code; never synchronises. */
 size_t dlmk_decode_block_workspace_size(int hidden_size, int q_dim, int kv_dim, int num_heads,
                                         int head_dim, int inter, int max_blocks_per_seq);

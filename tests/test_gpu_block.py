@@ -5,11 +5,12 @@ Mirrors the reference's device parity suite (tests/gpu_parity.rs): weights
 drawn by its SplitMix64 generator (uniform(-1, 1) * 0.05, unit norms), the
 same starting hidden states, several decode steps on two layers, and its
 tolerances on the hidden state -- 1e-3, or 2e-3 for int4 / int8 weights and
-the realistic width (gpu_parity.rs:114-116, :183, :218, :237).  Head dims are
-64 and 128, the f32 paged attention kernels' sizes (the reference's toy
-head_dim 8 / 16 configs are not supported by this path).  Each case starts at
-a 14-token history already in the pools so the steps cross a block boundary,
-on shuffled physical blocks.
+the realistic width (gpu_parity.rs:114-116, :183, :218, :237).  Head dims run
+from the reference's own toy configs (hidden 32 / head_dim 8,
+gpu_parity.rs:73-77; hidden 16 / head_dim 4, tests/speculative.rs:33-42) to 64,
+96 and 128, and GQA groups from 1 to 16.  Each case starts at a 14-token
+history already in the pools so the steps cross a block boundary, on shuffled
+physical blocks.
 """
 import numpy as np
 import pytest
@@ -71,6 +72,11 @@ CASES = [
     ("qkv-bias+llama3-rope", (256, 4, 2, 64, 512), W_F32, 1e-3, True,
      (500000.0, ("llama3", 8.0, 1.0, 4.0, 8192.0))),
     ("gqa8-bf16", (512, 8, 1, 64, 1024), W_BF16, 1e-3, False, (10000.0, None)),
+    ("gpu_parity-hidden32-d8", (32, 4, 2, 8, 64), W_F32, 1e-3, False, (10000.0, None)),
+    ("speculative-hidden16-d4", (16, 4, 2, 4, 32), W_F32, 1e-3, False, (10000.0, None)),
+    ("d96-gqa3", (384, 6, 2, 96, 512), W_F32, 1e-3, False, (10000.0, None)),
+    ("d80-bf16", (320, 4, 4, 80, 640), W_BF16, 1e-3, False, (10000.0, None)),
+    ("gqa16", (1024, 16, 1, 64, 512), W_F32, 1e-3, False, (10000.0, None)),
 ]
 
 

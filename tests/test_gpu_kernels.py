@@ -126,8 +126,20 @@ EDGE_CTX = [0, 1, 2, 15, 16, 17, 255, 256, 257, 511, 513, 1000]
 
 @pytest.mark.parametrize("dtype,Hq,Hkv,d,nq,ctx", [
     (np.float32, 32, 8, 64, 1, [576, 1, 300]),             # config-1 shape: 64-token partitions
-    (np.float32, 32, 8, 64, 1, EDGE_CTX),                   # small grid: 128-token partitions
+    (np.float32, 32, 8, 64, 1, EDGE_CTX),                   # 128-token partitions
     (np.float32, 32, 8, 64, 1, list(range(37, 1537, 37))),  # 40 seqs: 256-token partitions
+    (np.float32, 32, 8, 128, 1, [2049]),                    # the decode block's 8B shape
+    (np.float32, 128, 32, 128, 1, list(range(100, 4000, 197))),  # f32, 256-token partitions, d 128
+    # f32 geometries of any head dim (multiple of 4) and group: the generic kernel
+    (np.float32, 4, 2, 4, 1, [1, 17, 40]),                  # reference speculative tests' model
+    (np.float32, 4, 2, 8, 1, [1, 5, 33]),                   # reference gpu_parity.rs:73-77 shape
+    (np.float32, 6, 3, 12, 2, [2, 20, 77]),                 # 3 chunk rows
+    (np.float32, 12, 4, 80, 2, [2, 130, 1000]),
+    (np.float32, 32, 8, 96, 1, EDGE_CTX),
+    (np.float32, 64, 2, 64, 1, [300, 900]),                 # GQA 32: two row groups
+    (np.float32, 16, 4, 256, 1, [17, 900]),
+    (np.float32, 8, 8, 16, 4, [4, 16, 70]),
+    (np.float32, 48, 4, 20, 3, [3, 50, 600]),               # GQA 12 x 3 queries: 3 row groups
     (np.float16, 32, 8, 128, 1, EDGE_CTX),                  # config-2 shape
     (np.float16, 32, 8, 128, 1, [1023, 1024, 1025, 2048, 2049]),  # partition edges
     (np.float16, 32, 8, 128, 1, [9000, 100, 8193]),          # > 8 partitions: work-group combine
@@ -146,6 +158,13 @@ EDGE_CTX = [0, 1, 2, 15, 16, 17, 255, 256, 257, 511, 513, 1000]
     ("bf16", 32, 8, 128, 1, EDGE_CTX),                      # bf16 KV, 8B shape
     ("bf16", 32, 8, 128, 4, [4, 777]),
     ("bf16", 16, 8, 64, 1, [33, 600]),
+    # f16 / bf16 head dims and groups outside the tuned kernel's set
+    (np.float16, 32, 8, 96, 1, EDGE_CTX),
+    (np.float16, 16, 4, 80, 4, [4, 90, 1200]),
+    (np.float16, 64, 8, 128, 4, [4, 700, 2100]),            # GQA 8 x 4 queries: 2 row groups
+    (np.float16, 8, 2, 32, 1, [1, 40, 5000]),
+    (np.float16, 24, 8, 200, 2, [2, 1100]),
+    ("bf16", 24, 8, 96, 2, [2, 333, 1500]),
 ])
 def test_paged_attention_matches_oracle(oracle, torch_mod, ops, cuda, dtype, Hq, Hkv, d, nq,
                                         ctx):
@@ -280,9 +299,9 @@ def test_paged_attention_nan_workspace(oracle, torch_mod, ops, cuda, dtype, ctx,
 def test_paged_attention_unsupported_shape_raises(torch_mod, ops, cuda):
     torch = torch_mod
     from dlm_amd import DlmkError
-    q = torch.zeros((1, 1, 8, 96), dtype=torch.float16, device=cuda)
-    kp = torch.zeros((4, 8, 12, 16, 8), dtype=torch.float16, device=cuda)
-    vp = torch.zeros((4, 8, 96, 16), dtype=torch.float16, device=cuda)
+    q = torch.zeros((1, 1, 8, 264), dtype=torch.float16, device=cuda)  # head_dim above 256
+    kp = torch.zeros((4, 8, 33, 16, 8), dtype=torch.float16, device=cuda)
+    vp = torch.zeros((4, 8, 264, 16), dtype=torch.float16, device=cuda)
     t = torch.zeros((1, 4), dtype=torch.int32, device=cuda)
     with pytest.raises(DlmkError):
         ops.paged_decode_attention(q, kp, vp, t, t[:, 0].contiguous(), num_kv_heads=8)

@@ -18,6 +18,10 @@ pytestmark = pytest.mark.gpu
     (np.float32, 32, 8, 64, 1, [544, 1, 257]),                       # config-1 shape (VALU kernel)
     (np.float32, 16, 8, 64, 4, [3, 258, 600]),
     ("bf16", 32, 8, 128, 2, [2, 600, 1025]),
+    (np.float32, 4, 2, 8, 1, [1, 16, 17, 40]),                       # generic kernel, head_dim 8
+    (np.float32, 32, 8, 128, 2, [2, 300, 2049]),
+    (np.float16, 32, 8, 96, 2, [2, 17, 1100]),                       # generic f16, head_dim 96
+    (np.float16, 64, 8, 128, 4, [4, 513, 1030]),                     # two row groups
 ])
 def test_fused_step_equals_append_then_attention(oracle, cuda, dtype, Hq, Hkv, d, nq, ctx):
     import torch
