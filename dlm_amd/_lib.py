@@ -74,6 +74,9 @@ SIGNATURES = {
     "dlmk_decode_block_workspace_size": (_sz, [_i32] * 7),
     "dlmk_decode_block_paged": (_i32, [_vp] + [_i32] * 7 + [_f32, _i32, _i32] + [_vp] * 14 +
                                 [_vp, _vp, _i64, _vp, _i32, _i32, _i32, _vp, _sz]),
+    "dlmk_verify_block_workspace_size": (_sz, [_i32] * 8),
+    "dlmk_verify_block_paged": (_i32, [_vp] + [_i32] * 7 + [_f32, _i32, _i32] + [_vp] * 14 +
+                                [_vp, _vp, _i64, _vp, _i32, _i32, _i32, _i32, _vp, _sz]),
     "dlmk_paged_decode_attention": (_i32, [_vp, _vp, _i32, _vp, _vp, _vp, _i32, _vp, _vp, _i32,
                                            _i32, _i32, _i32, _i32, _i32, _i32, _i64, _f32, _vp,
                                            _sz]),

@@ -158,12 +158,14 @@ class PagedGpuKernel:
         for w in self.layers:
             _check_layer(cfg, w, w_dtype, self.w_group_size)
         self.max_blocks = max_blocks_per_seq
+        self.device = device
         self.inv_freq = torch.from_numpy(
             rope_inv_freqs(cfg.head_dim, cfg.rope_theta, cfg.rope_scaling)).to(device)
         nbytes = lib().dlmk_decode_block_workspace_size(
             cfg.hidden_size, cfg.q_dim, cfg.kv_dim, cfg.num_heads, cfg.head_dim,
             cfg.intermediate_size, max_blocks_per_seq)
         self.workspace = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        self._verify_ws = {}  # num_tokens -> workspace of dlmk_verify_block_paged
 
     # ComputeKernel surface (src/forward/kernel.rs:22-48)
     def num_layers(self) -> int:
@@ -175,18 +177,14 @@ class PagedGpuKernel:
     def kv_dim(self) -> int:
         return self.cfg.kv_dim
 
-    def run_block(self, layer: int, hidden: torch.Tensor, kv: Tuple[torch.Tensor, torch.Tensor],
-                  block_table: torch.Tensor, num_positions: int, position: int,
-                  stream=None) -> None:
-        """hidden: f32 [hidden_size] on the device, updated in place.  kv: this
-        layer's f32 pools; block_table: int32 [max_blocks] of the sequence."""
-        c, w = self.cfg, self.layers[layer]
+    def _check_kv(self, hidden: torch.Tensor, n: int, kv, block_table: torch.Tensor) -> None:
+        c = self.cfg
         k_pool, v_pool = kv
         for t, nm in ((hidden, "hidden"), (k_pool, "k_pool"), (v_pool, "v_pool"),
                       (block_table, "block_table")):
             _dev(t, nm)
-        if hidden.dtype != torch.float32 or hidden.numel() != c.hidden_size:
-            raise ValueError(f"hidden must be float32 [{c.hidden_size}]")
+        if hidden.dtype != torch.float32 or hidden.numel() != n * c.hidden_size:
+            raise ValueError(f"hidden must be float32 [{n} x {c.hidden_size}]")
         if k_pool.dtype != torch.float32 or v_pool.dtype != torch.float32:
             raise TypeError("the decode block's pools are float32 (dlm's KV history is f32)")
         tile = c.kv_dim * BLOCK_SIZE
@@ -194,15 +192,51 @@ class PagedGpuKernel:
             raise ValueError("pools must be [num_blocks, num_kv_heads, head_dim * 16] float32")
         if block_table.dtype != torch.int32 or block_table.numel() != self.max_blocks:
             raise ValueError(f"block_table must be int32 [{self.max_blocks}]")
+
+    def _weights(self, layer: int):
+        c, w = self.cfg, self.layers[layer]
+        return (c.hidden_size, c.q_dim, c.kv_dim, c.num_heads, c.num_kv_heads, c.head_dim,
+                c.intermediate_size, c.rms_eps, self.w_dtype, self.w_group_size,
+                _ptr(w.q_proj), _ptr(w.k_proj), _ptr(w.v_proj), _ptr(w.o_proj),
+                _ptr(w.gate_proj), _ptr(w.up_proj), _ptr(w.down_proj), _ptr(w.input_layernorm),
+                _ptr(w.post_attention_layernorm), _ptr(w.q_bias), _ptr(w.k_bias),
+                _ptr(w.v_bias), _ptr(self.inv_freq))
+
+    def run_block(self, layer: int, hidden: torch.Tensor, kv: Tuple[torch.Tensor, torch.Tensor],
+                  block_table: torch.Tensor, num_positions: int, position: int,
+                  stream=None) -> None:
+        """hidden: f32 [hidden_size] on the device, updated in place.  kv: this
+        layer's f32 pools; block_table: int32 [max_blocks] of the sequence."""
+        self._check_kv(hidden, 1, kv, block_table)
+        k_pool, v_pool = kv
+        tile = self.cfg.kv_dim * BLOCK_SIZE
         check(lib().dlmk_decode_block_paged(
-            _stream(stream), c.hidden_size, c.q_dim, c.kv_dim, c.num_heads, c.num_kv_heads,
-            c.head_dim, c.intermediate_size, c.rms_eps, self.w_dtype, self.w_group_size,
-            _ptr(w.q_proj), _ptr(w.k_proj), _ptr(w.v_proj), _ptr(w.o_proj), _ptr(w.gate_proj),
-            _ptr(w.up_proj), _ptr(w.down_proj), _ptr(w.input_layernorm),
-            _ptr(w.post_attention_layernorm), _ptr(w.q_bias), _ptr(w.k_bias), _ptr(w.v_bias),
-            _ptr(self.inv_freq), _ptr(hidden), _ptr(k_pool), _ptr(v_pool),
+            _stream(stream), *self._weights(layer), _ptr(hidden), _ptr(k_pool), _ptr(v_pool),
             k_pool.numel() // tile, _ptr(block_table), self.max_blocks, num_positions, position,
             _ptr(self.workspace), self.workspace.numel()))
+
+    def run_tokens(self, layer: int, hidden: torch.Tensor, kv: Tuple[torch.Tensor, torch.Tensor],
+                   block_table: torch.Tensor, num_positions: int, position: int,
+                   stream=None) -> None:
+        """run_block over n consecutive tokens in one pass (the batched verify
+        of a speculative round): hidden f32 [n, hidden_size], token j at
+        position num_positions + j, attending causally."""
+        n = hidden.shape[0] if hidden.dim() == 2 else 1
+        self._check_kv(hidden, n, kv, block_table)
+        ws = self._verify_ws.get(n)
+        if ws is None:
+            c = self.cfg
+            nbytes = lib().dlmk_verify_block_workspace_size(
+                c.hidden_size, c.q_dim, c.kv_dim, c.num_heads, c.head_dim, c.intermediate_size,
+                self.max_blocks, n)
+            ws = self._verify_ws[n] = torch.empty(max(nbytes, 256), dtype=torch.uint8,
+                                                  device=self.device)
+        k_pool, v_pool = kv
+        tile = self.cfg.kv_dim * BLOCK_SIZE
+        check(lib().dlmk_verify_block_paged(
+            _stream(stream), *self._weights(layer), _ptr(hidden), _ptr(k_pool), _ptr(v_pool),
+            k_pool.numel() // tile, _ptr(block_table), self.max_blocks, num_positions, position,
+            n, _ptr(ws), ws.numel()))
 
 
 def decode_token(kernel: PagedGpuKernel, cache, seq_id: int, hidden: torch.Tensor,

@@ -178,8 +178,8 @@ enum Epilogue { kAddInto = 1, kSwiGLU = 2, kRopeAppend = 3 };
 struct GemvSeg {
     const uint8_t *W, *W2;  // W2: the up projection of the SwiGLU epilogue
     const float *bias;      // kRopeAppend: may be null
-    float *out;
-    int rows;
+    float *out;             // token t's outputs start at out + t * ostride
+    int rows, ostride;
 };
 
 // kRopeAppend: segments q, k, v (+ biases); q is rotated in place into its
@@ -196,6 +196,7 @@ struct RopeArgs {
 struct GemvArgs {
     GemvSeg seg[3];
     int nseg, total_rows, in_dim, gs;
+    int nt;               // tokens (x rows [nt][in_dim]); the kernel's NT >= nt
     const float *x;
     const float *norm_w;  // non-null: x is staged as rmsnorm(x) * norm_w
     float eps;
@@ -232,10 +233,10 @@ struct RowGroup {  // RW launch rows resolved to their segments
 // layouts K [blk][Hkv][d/4][16][4], V [blk][Hkv][d][16]); a block id outside
 // the pool is skipped (the attention masks it).
 __device__ __forceinline__ void rope_store(const RopeArgs &r, int si, float *out, int row, float a,
-                                           float b) {
+                                           float b, int tok) {
     const int d = r.head_dim, half = d / 2, h = row / d, i = row % d;
     if (si < 2) {
-        const float ang = (float)r.position * r.inv_freq[i];
+        const float ang = (float)(r.position + tok) * r.inv_freq[i];
         const float sn = sinf(ang), cs = cosf(ang);
         const float ra = a * cs - b * sn, rb = a * sn + b * cs;
         a = ra;
@@ -246,9 +247,10 @@ __device__ __forceinline__ void rope_store(const RopeArgs &r, int si, float *out
         out[row + half] = b;
         return;
     }
-    const int64_t blk = r.table[r.num_positions / kBlock];
+    const int pos = r.num_positions + tok;
+    const int64_t blk = r.table[pos / kBlock];
     if (blk < 0 || blk >= r.num_blocks) return;
-    const int t = r.num_positions % kBlock;
+    const int t = pos % kBlock;
     const int64_t tile = (blk * r.num_kv_heads + h) * (int64_t)d * kBlock;
     if (si == 1) {
         float *kt = r.k_pool + tile;
@@ -261,13 +263,13 @@ __device__ __forceinline__ void rope_store(const RopeArgs &r, int si, float *out
     }
 }
 
-template <int DT, int EPI, int RW, int U>
+template <int DT, int EPI, int RW, int U, int NT>
 __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     using C = WChunk<DT>;
     constexpr int E = C::E;
     constexpr bool kTwo = EPI == kSwiGLU;
     extern __shared__ float xs[];
-    __shared__ float red[kGemvWaves];
+    __shared__ float red[NT][kGemvWaves];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int in_dim = a.in_dim;
     const int chunks = in_dim / E;
@@ -323,7 +325,7 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     };
 
     if constexpr (EPI == kRopeAppend)
-        if (blockIdx.x == 0 && threadIdx.x == 0) *a.rope.ctx_len = a.rope.num_positions + 1;
+        if (blockIdx.x == 0 && threadIdx.x == 0) *a.rope.ctx_len = a.rope.num_positions + a.nt;
     int r0 = (blockIdx.x * kGemvWaves + wave) * RW, c0 = 0;
     RowGroup<RW> RA, RB;
     u32x4 wa1[RW][U], wa2[RW][U], wb1[RW][U], wb2[RW][U];
@@ -339,10 +341,10 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     // as E/4 planes of float4, plane q holding elements 4q .. 4q + 3 of every
     // chunk: lanes reading consecutive chunks read consecutive 16-byte slots
     // (no bank conflicts; chunk-major storage conflicts 2-way for bf16 and
-    // more for the quantized dtypes).
+    // more for the quantized dtypes).  Token t's planes follow token t - 1's
+    // (t * in_dim floats in); tokens past nt are staged as zeros.
     constexpr int kStageUnroll = 8;
     const int n4 = in_dim / 4;
-    const float4 *x4 = reinterpret_cast<const float4 *>(a.x);
     float4 *xs4 = reinterpret_cast<float4 *>(xs);
     // The norm weights of this thread's first kNormPre normalise-pass slots,
     // loaded with x (not after the reduction's barrier).
@@ -358,38 +360,55 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
             }
         }
     }
-    float ss = 0.f;
-    for (int i0 = 0; i0 < n4; i0 += 64 * kGemvWaves * kStageUnroll) {
-        float4 v[kStageUnroll];
+    float ss[NT];
 #pragma unroll
-        for (int u = 0; u < kStageUnroll; ++u) {
-            const int i = i0 + u * 64 * kGemvWaves + threadIdx.x;
-            v[u] = i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
+    for (int t = 0; t < NT; ++t) {
+        ss[t] = 0.f;
+        const float4 *x4 = reinterpret_cast<const float4 *>(a.x) + (int64_t)t * n4;
+        float4 *xt4 = xs4 + t * n4;
+        const bool live = t < a.nt;
+        for (int i0 = 0; i0 < n4; i0 += 64 * kGemvWaves * kStageUnroll) {
+            float4 v[kStageUnroll];
 #pragma unroll
-        for (int u = 0; u < kStageUnroll; ++u) {
-            const int i = i0 + u * 64 * kGemvWaves + threadIdx.x;
-            if (i < n4) {
-                xs4[(i % (E / 4)) * chunks + i / (E / 4)] = v[u];
-                ss += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
+            for (int u = 0; u < kStageUnroll; ++u) {
+                const int i = i0 + u * 64 * kGemvWaves + threadIdx.x;
+                v[u] = live && i < n4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+#pragma unroll
+            for (int u = 0; u < kStageUnroll; ++u) {
+                const int i = i0 + u * 64 * kGemvWaves + threadIdx.x;
+                if (i < n4) {
+                    xt4[(i % (E / 4)) * chunks + i / (E / 4)] = v[u];
+                    ss[t] += v[u].x * v[u].x + v[u].y * v[u].y + v[u].z * v[u].z + v[u].w * v[u].w;
+                }
             }
         }
     }
     if (a.norm_w != nullptr) {
-        ss = wave_sum<64>(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        float tot = 0.f;
 #pragma unroll
-        for (int w = 0; w < kGemvWaves; ++w) tot += red[w];
-        const float inv = 1.0f / sqrtf(tot / (float)in_dim + a.eps);
+        for (int t = 0; t < NT; ++t) {
+            ss[t] = wave_sum<64>(ss[t]);
+            if (lane == 0) red[t][wave] = ss[t];
+        }
+        __syncthreads();
+        float inv[NT];
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            float tot = 0.f;
+#pragma unroll
+            for (int w = 0; w < kGemvWaves; ++w) tot += red[t][w];
+            inv[t] = 1.0f / sqrtf(tot / (float)in_dim + a.eps);
+        }
         auto norm4 = [&](int k, float4 w) {
-            float4 t = xs4[k];
-            t.x = t.x * inv * w.x;
-            t.y = t.y * inv * w.y;
-            t.z = t.z * inv * w.z;
-            t.w = t.w * inv * w.w;
-            xs4[k] = t;
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                float4 v = xs4[t * n4 + k];
+                v.x = v.x * inv[t] * w.x;
+                v.y = v.y * inv[t] * w.y;
+                v.z = v.z * inv[t] * w.z;
+                v.w = v.w * inv[t] * w.w;
+                xs4[t * n4 + k] = v;
+            }
         };
 #pragma unroll
         for (int j = 0; j < kNormPre; ++j) {
@@ -403,9 +422,11 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
     }
     __syncthreads();
 
-    float acc[RW], acc2[RW];
+    float acc[RW][NT], acc2[RW][NT];
 #pragma unroll
-    for (int j = 0; j < RW; ++j) acc[j] = acc2[j] = 0.f;
+    for (int j = 0; j < RW; ++j)
+#pragma unroll
+        for (int t = 0; t < NT; ++t) acc[j][t] = acc2[j][t] = 0.f;
 
     // One step: issue the next step's loads into (Rn, wn), then consume
     // (Rc, wc) at (r0, c0); finish the rows after their last chunk block.
@@ -427,51 +448,63 @@ __global__ __launch_bounds__(64 * kGemvWaves) void gemv_kernel(GemvArgs a) {
         for (int u = 0; u < U; ++u) {
             const int c = c0 + u * 64 + lane;
             if (c < chunks) {
-                float xv[E];  // this chunk's x, read once for the RW rows
 #pragma unroll
-                for (int q = 0; q < E / 4; ++q) {
-                    const float4 t = xs4[q * chunks + c];
-                    xv[4 * q] = t.x;
-                    xv[4 * q + 1] = t.y;
-                    xv[4 * q + 2] = t.z;
-                    xv[4 * q + 3] = t.w;
-                }
+                for (int t = 0; t < NT; ++t) {
+                    if (NT > 1 && t >= a.nt) break;
+                    float xv[E];  // token t's x of this chunk, read once for the RW rows
 #pragma unroll
-                for (int j = 0; j < RW; ++j) {
-                    const int64_t i0 = (int64_t)Rc.o[j] * in_dim + (int64_t)c * E;
-                    acc[j] += C::dot(wc1[j][u], xv, Rc.g[j].W, Rc.qo[j].scales, Rc.qo[j].zeros, a.gs, i0);
-                    if constexpr (kTwo)
-                        acc2[j] += C::dot(wc2[j][u], xv, Rc.g[j].W2, Rc.qo[j].scales, Rc.qo[j].zeros, a.gs, i0);
+                    for (int q = 0; q < E / 4; ++q) {
+                        const float4 v = xs4[t * n4 + q * chunks + c];
+                        xv[4 * q] = v.x;
+                        xv[4 * q + 1] = v.y;
+                        xv[4 * q + 2] = v.z;
+                        xv[4 * q + 3] = v.w;
+                    }
+#pragma unroll
+                    for (int j = 0; j < RW; ++j) {
+                        const int64_t i0 = (int64_t)Rc.o[j] * in_dim + (int64_t)c * E;
+                        acc[j][t] += C::dot(wc1[j][u], xv, Rc.g[j].W, Rc.qo[j].scales, Rc.qo[j].zeros, a.gs, i0);
+                        if constexpr (kTwo)
+                            acc2[j][t] += C::dot(wc2[j][u], xv, Rc.g[j].W2, Rc.qo[j].scales, Rc.qo[j].zeros, a.gs, i0);
+                    }
                 }
             }
         }
         if constexpr (EPI == kRopeAppend) {
             static_assert(RW == 2, "RoPE pairs need two rows per wave");
             if (last) {
-                float s[2];
 #pragma unroll
-                for (int j = 0; j < 2; ++j) {
-                    s[j] = wave_sum<64>(acc[j]);
-                    if (Rc.g[j].bias) s[j] += Rc.g[j].bias[Rc.o[j]];
-                    acc[j] = acc2[j] = 0.f;
+                for (int t = 0; t < NT; ++t) {
+                    float s[2];
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) {
+                        s[j] = wave_sum<64>(acc[j][t]);
+                        if (Rc.g[j].bias) s[j] += Rc.g[j].bias[Rc.o[j]];
+                        acc[j][t] = acc2[j][t] = 0.f;
+                    }
+                    if (lane == 0 && r0 < a.total_rows && t < a.nt)
+                        rope_store(a.rope, Rc.si[0], Rc.g[0].out + (int64_t)t * Rc.g[0].ostride, Rc.o[0],
+                                   s[0], s[1], t);
                 }
-                if (lane == 0 && r0 < a.total_rows) rope_store(a.rope, Rc.si[0], Rc.g[0].out, Rc.o[0], s[0], s[1]);
             }
         } else if (last) {
 #pragma unroll
-            for (int j = 0; j < RW; ++j) {
-                const float s1 = wave_sum<64>(acc[j]);
-                const float s2 = kTwo ? wave_sum<64>(acc2[j]) : 0.f;
-                if (lane == 0 && r0 + j < a.total_rows) {
-                    if constexpr (EPI == kAddInto) {
-                        Rc.g[j].out[Rc.o[j]] = Rc.g[j].out[Rc.o[j]] + s1;
-                    } else {
-                        // silu(gate) * up, cpu.rs:960-975
-                        Rc.g[j].out[Rc.o[j]] = s1 / (1.0f + expf(-s1)) * s2;
+            for (int t = 0; t < NT; ++t)
+#pragma unroll
+                for (int j = 0; j < RW; ++j) {
+                    const float s1 = wave_sum<64>(acc[j][t]);
+                    const float s2 = kTwo ? wave_sum<64>(acc2[j][t]) : 0.f;
+                    if (lane == 0 && r0 + j < a.total_rows && t < a.nt) {
+                        float *o = Rc.g[j].out + (int64_t)t * Rc.g[j].ostride + Rc.o[j];
+                        if constexpr (EPI == kAddInto) {
+                            *o = *o + s1;
+                        } else {
+                            // silu(gate) * up, cpu.rs:960-975
+                            *o = s1 / (1.0f + expf(-s1)) * s2;
+                        }
                     }
+                    acc[j][t] = acc2[j][t] = 0.f;
                 }
-                acc[j] = acc2[j] = 0.f;
-            }
         }
         r0 = r1;
         c0 = c1;
@@ -508,16 +541,13 @@ int device_cus() {
     return cus[dev];
 }
 
-// Resident work-groups: as many per compute unit as the LDS of the staged x
-// (and a cap of 8) allows, so that every work-group is running from the start
-// and each stages x once for all its rows.
 // Resident work-groups only (the occupancy of this instantiation with its
 // LDS), so every work-group runs from the start and stages x once for all
 // its rows.
-template <int DT, int EPI, int RW, int U>
+template <int DT, int EPI, int RW, int U, int NT>
 void launch_gemv_rw(hipStream_t st, const GemvArgs &a) {
-    const auto kernel = gemv_kernel<DT, EPI, RW, U>;
-    const size_t lds = (size_t)a.in_dim * sizeof(float);
+    const auto kernel = gemv_kernel<DT, EPI, RW, U, NT>;
+    const size_t lds = (size_t)NT * a.in_dim * sizeof(float);
     int per_cu = 0;
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, 64 * kGemvWaves, lds) !=
             hipSuccess || per_cu < 1)
@@ -529,39 +559,81 @@ void launch_gemv_rw(hipStream_t st, const GemvArgs &a) {
 
 // About 16 weight loads in flight per lane (8 per matrix for SwiGLU): rows of
 // at least 16 (8) loads per lane run one at a time, shorter rows 2 or 4 at once.
-template <int DT, int EPI>
+// Several tokens (NT > 1) do NT times the arithmetic per load and hold NT
+// accumulators per row: one row per wave (two for the RoPE pairs) and 16 / NT
+// (8 / NT) loads in flight, at least 2, keep them in registers.
+template <int DT, int EPI, int NT>
 void launch_gemv_epi(hipStream_t st, const GemvArgs &a) {
-    constexpr int T = EPI == kSwiGLU ? 8 : 16;
+    constexpr int T0 = EPI == kSwiGLU ? 8 : 16;
+    constexpr int T = NT == 1 ? T0 : (T0 / NT > 2 ? T0 / NT : 2);
     if constexpr (EPI == kRopeAppend) {
-        launch_gemv_rw<DT, EPI, 2, T / 2>(st, a);  // RoPE pairs: two rows per wave
+        launch_gemv_rw<DT, EPI, 2, (T / 2 > 1 ? T / 2 : 1), NT>(st, a);  // RoPE pairs: two rows per wave
+    } else if constexpr (NT > 1) {
+        launch_gemv_rw<DT, EPI, 1, T, NT>(st, a);
     } else {
         const int per_lane = (a.in_dim / WChunk<DT>::E + 63) / 64;  // chunk loads per lane per row
         if (per_lane >= T)
-            launch_gemv_rw<DT, EPI, 1, T>(st, a);
+            launch_gemv_rw<DT, EPI, 1, T, NT>(st, a);
         else if (per_lane >= T / 2)
-            launch_gemv_rw<DT, EPI, 2, T / 2>(st, a);
+            launch_gemv_rw<DT, EPI, 2, T / 2, NT>(st, a);
         else
-            launch_gemv_rw<DT, EPI, 4, T / 4>(st, a);
+            launch_gemv_rw<DT, EPI, 4, T / 4, NT>(st, a);
     }
 }
 
-template <int DT>
-void launch_gemv(int epi, hipStream_t st, const GemvArgs &a) {
+template <int DT, int NT>
+void launch_gemv_nt(int epi, hipStream_t st, const GemvArgs &a) {
     if (epi == kAddInto)
-        launch_gemv_epi<DT, kAddInto>(st, a);
+        launch_gemv_epi<DT, kAddInto, NT>(st, a);
     else if (epi == kSwiGLU)
-        launch_gemv_epi<DT, kSwiGLU>(st, a);
+        launch_gemv_epi<DT, kSwiGLU, NT>(st, a);
     else
-        launch_gemv_epi<DT, kRopeAppend>(st, a);
+        launch_gemv_epi<DT, kRopeAppend, NT>(st, a);
 }
 
-void gemv(int dt, int epi, hipStream_t st, const GemvArgs &a) {
+// Token counts the kernel is instantiated for; a launch of nt tokens runs
+// the smallest NT >= nt (tokens past nt are zeros and never stored).
+template <int DT>
+void launch_gemv(int epi, hipStream_t st, const GemvArgs &a) {
+    if (a.nt <= 1)
+        launch_gemv_nt<DT, 1>(epi, st, a);
+    else if (a.nt <= 2)
+        launch_gemv_nt<DT, 2>(epi, st, a);
+    else if (a.nt <= 4)
+        launch_gemv_nt<DT, 4>(epi, st, a);
+    else
+        launch_gemv_nt<DT, 8>(epi, st, a);
+}
+
+constexpr int kMaxTokensPerLaunch = 8;
+constexpr int64_t kGemvLdsMax = 64 * 1024;  // bytes of staged x per work-group
+
+void gemv_launch(int dt, int epi, hipStream_t st, const GemvArgs &a) {
     switch (dt) {
         case DLMK_W_F32: launch_gemv<DLMK_W_F32>(epi, st, a); break;
         case DLMK_W_BF16: launch_gemv<DLMK_W_BF16>(epi, st, a); break;
         case DLMK_W_F16: launch_gemv<DLMK_W_F16>(epi, st, a); break;
         case DLMK_W_INT4: launch_gemv<DLMK_W_INT4>(epi, st, a); break;
         default: launch_gemv<DLMK_W_INT8>(epi, st, a); break;
+    }
+}
+
+// n tokens through one GEMV stage: groups of as many tokens as one launch
+// stages in LDS (at most kMaxTokensPerLaunch), so every weight row is read
+// once per group -- the whole point of verifying a draft in one pass.
+void gemv(int dt, int epi, hipStream_t st, const GemvArgs &a, int n) {
+    const int64_t row_bytes = (int64_t)a.in_dim * sizeof(float);
+    int fit = (int)std::min<int64_t>(kMaxTokensPerLaunch, kGemvLdsMax / row_bytes);
+    // Whole instantiated NT sizes: 8, 4, 2, 1 (a padded NT also takes LDS).
+    fit = fit >= 8 ? 8 : fit >= 4 ? 4 : fit >= 2 ? 2 : 1;
+    for (int t0 = 0; t0 < n; t0 += fit) {
+        GemvArgs b = a;
+        b.nt = std::min(fit, n - t0);
+        b.x = a.x + (int64_t)t0 * a.in_dim;
+        for (int i = 0; i < b.nseg; ++i) b.seg[i].out += (int64_t)t0 * b.seg[i].ostride;
+        b.rope.num_positions += t0;
+        b.rope.position += t0;
+        gemv_launch(dt, epi, st, b);
     }
 }
 
@@ -575,64 +647,67 @@ GemvArgs gemv_args(const float *x, int in_dim, int gs, const float *norm_w, floa
     return a;
 }
 
-void add_seg(GemvArgs &a, const void *W, const void *W2, const float *bias, float *out, int rows) {
+// ostride: floats between consecutive tokens' outputs.
+void add_seg(GemvArgs &a, const void *W, const void *W2, const float *bias, float *out, int rows,
+             int ostride) {
     a.seg[a.nseg++] = GemvSeg{static_cast<const uint8_t *>(W), static_cast<const uint8_t *>(W2),
-                              bias, out, rows};
+                              bias, out, rows, ostride};
     a.total_rows += rows;
 }
 
-// Workspace regions, each on a 256-byte boundary: q[qd], k[kvd], v[kvd],
-// ctx[qd], act[inter], ctx_len (int32), then the attention workspace.
+// Workspace regions, each on a 256-byte boundary, for n tokens: q[n][qd],
+// k[kvd], v[kvd] (the k / v segments' outputs go to the pools; these are
+// never written), ctx[n][qd], act[n][inter], ctx_len (int32), then the
+// attention workspace.
 struct BlockWs {
     int64_t q, k, v, ctx, act, ctx_len, attn, total;
 };
 
-BlockWs block_ws(int qd, int kvd, int inter, int64_t attn_bytes) {
+BlockWs block_ws(int qd, int kvd, int inter, int n, int64_t attn_bytes) {
     const auto up = [](int64_t x) { return (x + 255) / 256 * 256; };
     BlockWs w;
     w.q = 0;
-    w.k = up(w.q + 4LL * qd);
+    w.k = up(w.q + 4LL * qd * n);
     w.v = up(w.k + 4LL * kvd);
     w.ctx = up(w.v + 4LL * kvd);
-    w.act = up(w.ctx + 4LL * qd);
-    w.ctx_len = up(w.act + 4LL * inter);
+    w.act = up(w.ctx + 4LL * qd * n);
+    w.ctx_len = up(w.act + 4LL * inter * n);
     w.attn = up(w.ctx_len + 4);
     w.total = w.attn + attn_bytes;
     return w;
 }
 
-}  // namespace
-
-extern "C" {
-
-size_t dlmk_decode_block_workspace_size(int hidden_size, int q_dim, int kv_dim, int num_heads,
-                                        int head_dim, int inter, int max_blocks_per_seq) {
+size_t block_workspace_size(int hidden_size, int q_dim, int kv_dim, int num_heads, int head_dim,
+                            int inter, int max_blocks_per_seq, int n) {
     if (hidden_size <= 0 || q_dim <= 0 || kv_dim <= 0 || num_heads <= 0 || head_dim <= 0 ||
-        inter <= 0 || max_blocks_per_seq <= 0)
+        inter <= 0 || max_blocks_per_seq <= 0 || n <= 0)
         return 0;
-    const size_t attn = dlmk_paged_attention_workspace_size(1, 1, num_heads, head_dim, kBlock,
+    const size_t attn = dlmk_paged_attention_workspace_size(1, n, num_heads, head_dim, kBlock,
                                                             max_blocks_per_seq);
-    return (size_t)block_ws(q_dim, kv_dim, inter, (int64_t)attn).total;
+    return (size_t)block_ws(q_dim, kv_dim, inter, n, (int64_t)attn).total;
 }
 
-int dlmk_decode_block_paged(
-    void *stream, int hidden_size, int q_dim, int kv_dim, int num_heads, int num_kv_heads,
-    int head_dim, int inter, float rms_eps, int w_dtype, int w_group_size, const void *q_proj,
-    const void *k_proj, const void *v_proj, const void *o_proj, const void *gate_proj,
-    const void *up_proj, const void *down_proj, const float *in_norm, const float *post_norm,
-    const float *q_bias, const float *k_bias, const float *v_bias, const float *inv_freq,
-    float *x, void *k_pool, void *v_pool, int64_t num_blocks, const int32_t *block_table,
-    int max_blocks_per_seq, int num_positions, int position, void *workspace,
-    size_t workspace_bytes) {
-    static const char *who = "dlmk_decode_block_paged";
+// dlmk_decode_block_paged (n = 1) and dlmk_verify_block_paged: n consecutive
+// tokens at positions num_positions .. num_positions + n - 1 (RoPE angles
+// from position .. position + n - 1), x [n][hidden] in place.
+int block_impl(const char *who, void *stream, int hidden_size, int q_dim, int kv_dim,
+               int num_heads, int num_kv_heads, int head_dim, int inter, float rms_eps,
+               int w_dtype, int w_group_size, const void *q_proj, const void *k_proj,
+               const void *v_proj, const void *o_proj, const void *gate_proj, const void *up_proj,
+               const void *down_proj, const float *in_norm, const float *post_norm,
+               const float *q_bias, const float *k_bias, const float *v_bias,
+               const float *inv_freq, float *x, void *k_pool, void *v_pool, int64_t num_blocks,
+               const int32_t *block_table, int max_blocks_per_seq, int num_positions,
+               int position, int n, void *workspace, size_t workspace_bytes) {
     if (hidden_size <= 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || inter <= 0 ||
-        max_blocks_per_seq <= 0 || num_positions < 0 || num_blocks < 1 ||
+        max_blocks_per_seq <= 0 || num_positions < 0 || num_blocks < 1 || n < 1 ||
         q_dim != num_heads * head_dim || kv_dim != num_kv_heads * head_dim ||
         num_heads % num_kv_heads != 0 || head_dim % 2 != 0)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: inconsistent sizes", who);
-    if ((int64_t)num_positions + 1 > (int64_t)max_blocks_per_seq * kBlock)
-        return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: position %d beyond the block table (%d blocks)",
-                          who, num_positions, max_blocks_per_seq);
+    if ((int64_t)num_positions + n > (int64_t)max_blocks_per_seq * kBlock)
+        return dlmk::fail(DLMK_ERR_INVALID_ARG,
+                          "%s: positions %d..%d beyond the block table (%d blocks)", who,
+                          num_positions, num_positions + n - 1, max_blocks_per_seq);
     if (!q_proj || !k_proj || !v_proj || !o_proj || !gate_proj || !up_proj || !down_proj ||
         !in_norm || !post_norm || !inv_freq || !x || !k_pool || !v_pool || !block_table)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: null pointer", who);
@@ -644,12 +719,12 @@ int dlmk_decode_block_paged(
                           "%s: hidden %d, q_dim %d, inter %d%s must be multiples of %d", who,
                           hidden_size, q_dim, inter, quant ? " and the group size" : "", E);
     const int64_t lds_max = (int64_t)std::max(hidden_size, std::max(q_dim, inter)) * 4;
-    if (lds_max > 64 * 1024)
+    if (lds_max > kGemvLdsMax)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED, "%s: input width %lld floats exceeds LDS", who,
                           (long long)(lds_max / 4));
-    const size_t attn_need = dlmk_paged_attention_workspace_size(1, 1, num_heads, head_dim, kBlock,
+    const size_t attn_need = dlmk_paged_attention_workspace_size(1, n, num_heads, head_dim, kBlock,
                                                                  max_blocks_per_seq);
-    const BlockWs ws = block_ws(q_dim, kv_dim, inter, (int64_t)attn_need);
+    const BlockWs ws = block_ws(q_dim, kv_dim, inter, n, (int64_t)attn_need);
     if (!workspace || (int64_t)workspace_bytes < ws.total)
         return dlmk::fail(DLMK_ERR_WORKSPACE, "%s: workspace %zu bytes, need %lld", who,
                           workspace_bytes, (long long)ws.total);
@@ -668,36 +743,88 @@ int dlmk_decode_block_paged(
 
     // Attention sublayer: rmsnorm folded into the q/k/v launch's staging.
     GemvArgs qkv = gemv_args(x, hidden_size, gs, in_norm, rms_eps);
-    add_seg(qkv, q_proj, nullptr, q_bias, q, q_dim);
-    add_seg(qkv, k_proj, nullptr, k_bias, k, kv_dim);
-    add_seg(qkv, v_proj, nullptr, v_bias, v, kv_dim);
+    add_seg(qkv, q_proj, nullptr, q_bias, q, q_dim, q_dim);
+    add_seg(qkv, k_proj, nullptr, k_bias, k, kv_dim, 0);
+    add_seg(qkv, v_proj, nullptr, v_bias, v, kv_dim, 0);
     // RoPE and the append are the launch's epilogue (rows paired per head).
     qkv.rope = RopeArgs{inv_freq, static_cast<float *>(k_pool), static_cast<float *>(v_pool),
                         block_table, num_blocks, num_kv_heads, head_dim, num_positions, position,
                         ctx_len};
-    gemv(w_dtype, kRopeAppend, st, qkv);
+    gemv(w_dtype, kRopeAppend, st, qkv, n);
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return dlmk::fail((int)e, "%s launch: %s", who, hipGetErrorString(e));
+    // n causal queries: token j sees positions 0 .. num_positions + j.
     const int rc = dlmk_paged_decode_attention(
-        stream, ctx, DLMK_F32, q, k_pool, v_pool, DLMK_F32, block_table, ctx_len, 1, 1, num_heads,
+        stream, ctx, DLMK_F32, q, k_pool, v_pool, DLMK_F32, block_table, ctx_len, 1, n, num_heads,
         num_kv_heads, head_dim, kBlock, max_blocks_per_seq, num_blocks,
         1.0f / sqrtf((float)head_dim), attn_need ? base + ws.attn : nullptr, attn_need);
     if (rc != DLMK_OK) return rc;
     GemvArgs oproj = gemv_args(ctx, q_dim, gs, nullptr, 0.f);
-    add_seg(oproj, o_proj, nullptr, nullptr, x, hidden_size);
-    gemv(w_dtype, kAddInto, st, oproj);
+    add_seg(oproj, o_proj, nullptr, nullptr, x, hidden_size, hidden_size);
+    gemv(w_dtype, kAddInto, st, oproj, n);
 
     // MLP sublayer (SwiGLU): the post-attention rmsnorm folded into the
     // gate/up launch's staging.
     GemvArgs gu = gemv_args(x, hidden_size, gs, post_norm, rms_eps);
-    add_seg(gu, gate_proj, up_proj, nullptr, act, inter);
-    gemv(w_dtype, kSwiGLU, st, gu);
+    add_seg(gu, gate_proj, up_proj, nullptr, act, inter, inter);
+    gemv(w_dtype, kSwiGLU, st, gu, n);
     GemvArgs down = gemv_args(act, inter, gs, nullptr, 0.f);
-    add_seg(down, down_proj, nullptr, nullptr, x, hidden_size);
-    gemv(w_dtype, kAddInto, st, down);
+    add_seg(down, down_proj, nullptr, nullptr, x, hidden_size, hidden_size);
+    gemv(w_dtype, kAddInto, st, down, n);
     e = hipGetLastError();
     if (e != hipSuccess) return dlmk::fail((int)e, "%s launch: %s", who, hipGetErrorString(e));
     return DLMK_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t dlmk_decode_block_workspace_size(int hidden_size, int q_dim, int kv_dim, int num_heads,
+                                        int head_dim, int inter, int max_blocks_per_seq) {
+    return block_workspace_size(hidden_size, q_dim, kv_dim, num_heads, head_dim, inter,
+                                max_blocks_per_seq, 1);
+}
+
+int dlmk_decode_block_paged(
+    void *stream, int hidden_size, int q_dim, int kv_dim, int num_heads, int num_kv_heads,
+    int head_dim, int inter, float rms_eps, int w_dtype, int w_group_size, const void *q_proj,
+    const void *k_proj, const void *v_proj, const void *o_proj, const void *gate_proj,
+    const void *up_proj, const void *down_proj, const float *in_norm, const float *post_norm,
+    const float *q_bias, const float *k_bias, const float *v_bias, const float *inv_freq,
+    float *x, void *k_pool, void *v_pool, int64_t num_blocks, const int32_t *block_table,
+    int max_blocks_per_seq, int num_positions, int position, void *workspace,
+    size_t workspace_bytes) {
+    return block_impl("dlmk_decode_block_paged", stream, hidden_size, q_dim, kv_dim, num_heads,
+                      num_kv_heads, head_dim, inter, rms_eps, w_dtype, w_group_size, q_proj,
+                      k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj, in_norm, post_norm,
+                      q_bias, k_bias, v_bias, inv_freq, x, k_pool, v_pool, num_blocks,
+                      block_table, max_blocks_per_seq, num_positions, position, 1, workspace,
+                      workspace_bytes);
+}
+
+size_t dlmk_verify_block_workspace_size(int hidden_size, int q_dim, int kv_dim, int num_heads,
+                                        int head_dim, int inter, int max_blocks_per_seq,
+                                        int num_tokens) {
+    return block_workspace_size(hidden_size, q_dim, kv_dim, num_heads, head_dim, inter,
+                                max_blocks_per_seq, num_tokens);
+}
+
+int dlmk_verify_block_paged(
+    void *stream, int hidden_size, int q_dim, int kv_dim, int num_heads, int num_kv_heads,
+    int head_dim, int inter, float rms_eps, int w_dtype, int w_group_size, const void *q_proj,
+    const void *k_proj, const void *v_proj, const void *o_proj, const void *gate_proj,
+    const void *up_proj, const void *down_proj, const float *in_norm, const float *post_norm,
+    const float *q_bias, const float *k_bias, const float *v_bias, const float *inv_freq,
+    float *x, void *k_pool, void *v_pool, int64_t num_blocks, const int32_t *block_table,
+    int max_blocks_per_seq, int num_positions, int position, int num_tokens, void *workspace,
+    size_t workspace_bytes) {
+    return block_impl("dlmk_verify_block_paged", stream, hidden_size, q_dim, kv_dim, num_heads,
+                      num_kv_heads, head_dim, inter, rms_eps, w_dtype, w_group_size, q_proj,
+                      k_proj, v_proj, o_proj, gate_proj, up_proj, down_proj, in_norm, post_norm,
+                      q_bias, k_bias, v_bias, inv_freq, x, k_pool, v_pool, num_blocks,
+                      block_table, max_blocks_per_seq, num_positions, position, num_tokens,
+                      workspace, workspace_bytes);
 }
 
 }  // extern "C"

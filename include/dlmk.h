@@ -359,6 +359,36 @@ int dlmk_decode_block_paged(
     int max_blocks_per_seq, int num_positions, int position, void *workspace,
     size_t workspace_bytes);
 
+/* The decode block over num_tokens consecutive tokens in one pass: the
+ * batched target verify of a speculative round.  dlm verifies a draft one
+ * token at a time, re-running the target per position
+ * (SpeculativeSession::step, src/speculative.rs:145-185); this runs the
+ * gamma + 1 tokens [last, d1 .. d_gamma] through a layer together.  Same
+ * arguments as dlmk_decode_block_paged plus num_tokens (>= 1): x is
+ * [num_tokens][hidden] (updated in place); token j's K/V go to position
+ * num_positions + j and its RoPE angle uses position + j; token j attends
+ * causally to positions 0 .. num_positions + j (dlmk_paged_decode_attention
+ * with num_q_per_seq = num_tokens).  Each GEMV stage reads its weights once
+ * per group of up to 8 tokens whose inputs fit 64 KiB of LDS together (one
+ * token at a time for inputs wider than 8192 floats).  The result per token
+ * is the sequential decode block's up to float rounding.  Workspace:
+ * dlmk_verify_block_workspace_size(..., num_tokens) bytes, 256-byte aligned.
+ * No counterpart in the reference's FFI; rejected tokens are rolled back by
+ * the caller (dlmk_cache_truncate_sequence) -- their pool slots are simply
+ * overwritten by the next append. */
+size_t dlmk_verify_block_workspace_size(int hidden_size, int q_dim, int kv_dim, int num_heads,
+                                        int head_dim, int inter, int max_blocks_per_seq,
+                                        int num_tokens);
+int dlmk_verify_block_paged(
+    void *stream, int hidden_size, int q_dim, int kv_dim, int num_heads, int num_kv_heads,
+    int head_dim, int inter, float rms_eps, int w_dtype, int w_group_size, const void *q_proj,
+    const void *k_proj, const void *v_proj, const void *o_proj, const void *gate_proj,
+    const void *up_proj, const void *down_proj, const float *in_norm, const float *post_norm,
+    const float *q_bias, const float *k_bias, const float *v_bias, const float *inv_freq,
+    float *x, void *k_pool, void *v_pool, int64_t num_blocks, const int32_t *block_table,
+    int max_blocks_per_seq, int num_positions, int position, int num_tokens, void *workspace,
+    size_t workspace_bytes);
+
 /* Pinned host memory, PinnedBuffer (src/memory/pinned.rs:38-112) analogue.
  * dlmk_alloc_pinned: page-locked, zero-initialised, rounded up to whole 4 KiB
  * pages (PinnedBuffer::with_len, pinned.rs:59-67); bytes == 0 returns
