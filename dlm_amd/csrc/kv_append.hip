@@ -203,17 +203,65 @@ __device__ __forceinline__ void load8(const S *p, float (&x)[8]) {
     }
 }
 
-__device__ __forceinline__ int quant_code(float x, float inv_ok, float scale, float qmax) {
-    const float r = roundf(x / scale);
-    return (inv_ok == 0.f || r != r) ? 0 : (int)fminf(fmaxf(r, -qmax), qmax);
+// The 8 codes of a chunk, packed as stored (offset binary): int8 w0 = bytes
+// c0..c3 + 128, w1 = c4..c7 + 128; int4 w0 byte m = (c_2m + 8) | (c_2m+1 + 8)
+// << 4, where c = clamp(round(x / scale), -qmax, qmax) (round half away
+// from zero; NaN quotients and scale 0 give 0).  No division per element:
+// Ziv's rounding test (A. Ziv, "Fast evaluation of elementary
+// mathematical functions with correctly rounded last bit", ACM TOMS 17(3),
+// 1991) -- evaluate cheaply with a known error bound, and take the exact path
+// only when the bound cannot decide the rounding.  inv = 1 / scale is
+// correctly rounded and |x| <= max, so y = x * inv differs from x / scale by
+// at most |x / scale| 2^-23 <= 128 2^-23 = 2^-16, and the rounded quotient
+// fl(x / scale) from x / scale by at most half an ulp, 2^-17.  roundf and
+// rintf agree except at the half-integers, and change value only there; so
+// when y is more than 2^-14 away from every half-integer (|y - rint(y)| <
+// 1/2 - 2^-14), rint(y) == roundf(fl(x / scale)).  Otherwise -- about 2^-13
+// of the elements, and every non-finite y (NaN input, scale 0 or a scale
+// whose reciprocal overflows: then y is NaN or infinite) -- the chunk takes
+// the division.  Codes are packed with v_cvt_pk_u8_f32.
+template <int QBITS>
+__device__ __forceinline__ void quant_chunk(const float (&x)[8], float inv_ok, float scale,
+                                            float inv, uint32_t &w0, uint32_t &w1) {
+    constexpr float qmax = QBITS == 8 ? 127.f : 7.f, bias = QBITS == 8 ? 128.f : 8.f;
+    float r[8];
+    bool exact = true;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        const float y = x[k] * inv;
+        r[k] = __builtin_rintf(y);
+        exact = exact && fabsf(y - r[k]) < 0.5f - 0x1p-14f;
+    }
+    if (!exact) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float q = roundf(x[k] / scale);
+            r[k] = (inv_ok == 0.f || q != q) ? 0.f : q;
+        }
+    }
+    float c[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) c[k] = __builtin_amdgcn_fmed3f(r[k], -qmax, qmax) + bias;
+    if constexpr (QBITS == 8) {
+        w0 = w1 = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            w0 = __builtin_amdgcn_cvt_pk_u8_f32(c[k], k, w0);
+            w1 = __builtin_amdgcn_cvt_pk_u8_f32(c[4 + k], k, w1);
+        }
+    } else {
+        w0 = w1 = 0;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) w0 = __builtin_amdgcn_cvt_pk_u8_f32(fmaf(c[2 * m + 1], 16.f, c[2 * m]), m, w0);
+    }
 }
 
-// Stores the 8 offset-binary codes q of dims j .. j + 7 of token t into the
-// (block, kv head) tile at `tile` (K if which == 0, else V), in the layouts
-// described above.
+// Stores a chunk's packed codes (quant_chunk) of dims j .. j + 7 of token t
+// into the (block, kv head) tile at `tile` (K if which == 0, else V), in the
+// layouts described above.
 template <int QBITS>
 __device__ __forceinline__ void place_chunk(uint8_t *tile, int which, int j, int t, int d,
-                                            const int (&q)[8]) {
+                                            uint32_t w0, uint32_t w1) {
     constexpr int BS = 16;
     const int KG = QBITS == 8 ? 16 : (d % 128 == 0 ? 32 : 16);
     const int VG = QBITS == 8 ? 4 : (d % 128 == 0 ? 8 : 4);
@@ -224,29 +272,25 @@ __device__ __forceinline__ void place_chunk(uint8_t *tile, int which, int j, int
     uint8_t *vbase = tile + ((int64_t)(vq * 4 + t / 4) * 16 + vn) * VLANE + t % 4;
     if constexpr (QBITS == 8) {
         if (which == 0) {
-            u32x2 w;
-            w[0] = (q[0] & 0xff) | (q[1] & 0xff) << 8 | (q[2] & 0xff) << 16 | (uint32_t)(q[3] & 0xff) << 24;
-            w[1] = (q[4] & 0xff) | (q[5] & 0xff) << 8 | (q[6] & 0xff) << 16 | (uint32_t)(q[7] & 0xff) << 24;
-            *reinterpret_cast<u32x2 *>(tile + ((j / KG) * BS + t) * KG + j % KG) = w;
+            *reinterpret_cast<u32x2 *>(tile + ((j / KG) * BS + t) * KG + j % KG) = u32x2{w0, w1};
         } else {
             // 8 dims = two lane groups of VG = 4 (vk == 0).
 #pragma unroll
-            for (int k = 0; k < 8; ++k) vbase[(k / 4) * VLANE + (k % 4) * 4] = (uint8_t)q[k];
+            for (int k = 0; k < 4; ++k) {
+                vbase[k * 4] = (uint8_t)(w0 >> (8 * k));
+                vbase[VLANE + k * 4] = (uint8_t)(w1 >> (8 * k));
+            }
         }
     } else {
-        uint8_t by[4];
-#pragma unroll
-        for (int m = 0; m < 4; ++m) by[m] = (uint8_t)((q[2 * m] & 0x0f) | (q[2 * m + 1] & 0x0f) << 4);
         if (which == 0) {
-            uint32_t w = by[0] | by[1] << 8 | by[2] << 16 | (uint32_t)by[3] << 24;
-            *reinterpret_cast<uint32_t *>(tile + ((j / KG) * BS + t) * (KG / 2) + (j % KG) / 2) = w;
+            *reinterpret_cast<uint32_t *>(tile + ((j / KG) * BS + t) * (KG / 2) + (j % KG) / 2) = w0;
         } else {
             // Dim pair m of the chunk: VG = 8 keeps the chunk in one lane
             // group (words vk/2 .. +3); VG = 4 spans two (vk == 0).
 #pragma unroll
             for (int m = 0; m < 4; ++m) {
                 const int jj = vk + 2 * m;
-                vbase[(jj / VG) * VLANE + ((jj % VG) / 2) * 4] = by[m];
+                vbase[(jj / VG) * VLANE + ((jj % VG) / 2) * 4] = (uint8_t)(w0 >> (8 * m));
             }
         }
     }
@@ -297,6 +341,7 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
         mx = fmaxf(red[2 * which], red[2 * which + 1]);
         const float scale = mx / qmax;
         const float ok = scale > 0.f ? 1.f : 0.f;
+        const float inv = 1.0f / scale;
         if (lt == 0) (which ? v_scales : k_scales)[slot] = ok != 0.f ? scale : 0.f;
 #pragma unroll
         for (int i = 0; i < NC; ++i) {
@@ -304,11 +349,9 @@ __global__ __launch_bounds__(256) void kv_append_quant_kernel(
             if (c >= nchunks) continue;
             const int h = (8 * c) / d, j = 8 * c - h * d;
             uint8_t *tile = pool + (blk * num_kv_heads + h) * tile_bytes;
-            int q[8];
-#pragma unroll
-            // Offset binary in the pools: code c is stored as c + 128 (c + 8).
-            for (int k = 0; k < 8; ++k) q[k] = quant_code(x[i][k], ok, scale, qmax) + (QBITS == 8 ? 128 : 8);
-            place_chunk<QBITS>(tile, which, j, t, d, q);
+            uint32_t w0, w1;
+            quant_chunk<QBITS>(x[i], ok, scale, inv, w0, w1);
+            place_chunk<QBITS>(tile, which, j, t, d, w0, w1);
         }
     }
 }
@@ -387,69 +430,128 @@ extern "C" int dlmk_kv_append(void *stream, void *k_pool, void *v_pool, const vo
     return DLMK_OK;
 }
 
-// Prefill-sized int8 appends: one work-group per run of 16 consecutive
-// source tokens, 512 threads (256 per pool; 16 lanes per token, RC chunks
-// each, so a token's max is a 16-lane shuffle reduction).  When the run's
-// slots fill one block in order, the codes are placed into an LDS image of
-// the block's tiles (every kv head) and the image is copied out with 16-byte
-// stores; otherwise each thread places its codes straight into the pool.
-constexpr int kQuantRunMaxKvDim = 1024;
-constexpr int64_t kQuantRunMinTokens = 512;
+// Quantizing appends of kQuadMinTokens or more (kv_dim <= 4096): one
+// work-group per quad of 4 consecutive source tokens and one pool (grid.y: K
+// or V), kQuadWaves waves.  Lane (e, sub) of wave w holds token e's 8-dim
+// chunks sub + 16 (w + kQuadWaves i), i < RC.  A token's max is a 16-lane
+// shuffle reduction, then a max over the waves in LDS.  Codes come from
+// quant_chunk.  K chunks are one 8-byte (int8) or 4-byte (int4) store per
+// lane, as place_chunk does.  A V word holds one dim (int8) or dim pair
+// (int4) of a token quad (V layout above), so when the 4 tokens fill one quad
+// of one block (slots s .. s + 3, s % 4 == 0), the 4 lanes sharing a chunk
+// transpose their packed codes (4 x 4 bytes, lane shuffles) and each stores
+// whole words; otherwise V bytes are stored as place_chunk does.
+// Measured at configs[2] (2096 tokens, kv_dim 1024, f16 source), bench.py
+// graph replays, int8 / int4:
+//   LDS image of whole blocks (byte stores, 72% of its LDS cycles bank
+//   conflicts by SQ_LDS_BANK_CONFLICT / SQ_LDS_IDX_ACTIVE) / one work-group
+//   per token: 11.6 / 8.5 us;
+//   1 wave per quad (16 lanes per token, 64 elements a lane, ~4500
+//   instructions in one dependent chain): 11.4 / 12.1 us;
+//   8 waves: 9.3 / 8.4 us; 4 waves (2 chunks a lane): 7.0 / 6.9 us;
+//   2 waves: 7.5 / 7.8 us.
+// Decode-sized appends (64 tokens) are faster one work-group per token
+// (3.4 / 3.2 us against 4.6 / 3.6 us).
+#ifndef DLMK_QUAD_WAVES
+#define DLMK_QUAD_WAVES 4
+#endif
+constexpr int kQuadWaves = DLMK_QUAD_WAVES;
+#ifndef DLMK_QUAD_MIN_TOKENS
+#define DLMK_QUAD_MIN_TOKENS 256
+#endif
+constexpr int64_t kQuadMinTokens = DLMK_QUAD_MIN_TOKENS;
+
+// Lanes sub + 16 t (t = 0..3) hold token t's packed word a; lane sub + 16 e
+// gets word e of the transpose: byte t = byte e of token t's word.
+__device__ __forceinline__ uint32_t quad_transpose(uint32_t a, int e, int sub) {
+    uint32_t r = 0;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const uint32_t at = (uint32_t)__shfl((int)a, sub + 16 * t, 64);
+        r |= ((at >> (8 * e)) & 0xffu) << (8 * t);
+    }
+    return r;
+}
 
 template <int QBITS, typename S, int RC>
-__global__ __launch_bounds__(512) void kv_append_quant_run_kernel(
+__global__ __launch_bounds__(64 * kQuadWaves) void kv_append_quant_quad_kernel(
     uint8_t *__restrict__ k_pool, uint8_t *__restrict__ v_pool, float *__restrict__ k_scales,
     float *__restrict__ v_scales, const S *__restrict__ k_src, const S *__restrict__ v_src,
     const int64_t *__restrict__ slots, int64_t n_tok, int num_kv_heads, int head_dim,
     int64_t num_slots) {
     constexpr int BS = 16;
-    __shared__ __attribute__((aligned(16))) uint8_t img[2][kQuantRunMaxKvDim * BS * QBITS / 8];
-    const int which = threadIdx.x >> 8, lt = threadIdx.x & 255, tt = lt >> 4, sub = lt & 15;
-    const int64_t tok0 = (int64_t)blockIdx.x * BS, tok = tok0 + tt;
+    __shared__ float red[kQuadWaves][4];
+    const int which = blockIdx.y;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, e = lane >> 4, sub = lane & 15;
+    const int64_t tok = (int64_t)blockIdx.x * 4 + e;
     const bool have = tok < n_tok;
-    const int d = head_dim, kv_dim = num_kv_heads * head_dim;
-    const float qmax = QBITS == 8 ? 127.f : 7.f;
-    const S *src = (which ? v_src : k_src) + (have ? tok : tok0) * kv_dim;
+    const int64_t slot = have ? slots[tok] : -1;
+    const int d = head_dim, kv_dim = num_kv_heads * head_dim, nchunks = kv_dim / 8;
+    constexpr float qmax = QBITS == 8 ? 127.f : 7.f;
+    const S *src = (which ? v_src : k_src) + (have ? tok : 0) * (int64_t)kv_dim;
     float x[RC][8];
     float mx = 0.f;
 #pragma unroll
     for (int i = 0; i < RC; ++i) {
-        load8(src + 8 * (sub + 16 * i), x[i]);
+        const int c = sub + 16 * (wave + kQuadWaves * i);
+        if (have && c < nchunks) {
+            load8(src + 8 * c, x[i]);
+        } else {
+#pragma unroll
+            for (int k = 0; k < 8; ++k) x[i][k] = 0.f;
+        }
 #pragma unroll
         for (int k = 0; k < 8; ++k) mx = fmaxf(mx, fabsf(x[i][k]));
     }
 #pragma unroll
     for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    const int64_t slot = have ? slots[tok] : -1;
-    const int64_t slot0 = slots[tok0];  // tok0 < n_tok: the grid is ceil(n_tok / 16) runs
-    const bool in_run = have && slot0 >= 0 && slot0 % BS == 0 && slot0 + BS <= num_slots && slot == slot0 + tt;
-    const bool full = __syncthreads_and(in_run);
+    if (sub == 0) red[wave][e] = mx;
+    __syncthreads();
+#pragma unroll
+    for (int w = 0; w < kQuadWaves; ++w) mx = fmaxf(mx, red[w][e]);
     const bool valid = have && slot >= 0 && slot < num_slots;
     const float scale = mx / qmax;
     const float ok = scale > 0.f ? 1.f : 0.f;
-    if (valid && sub == 0) (which ? v_scales : k_scales)[slot] = ok != 0.f ? scale : 0.f;
+    const float inv = 1.0f / scale;
+    if (valid && wave == 0 && sub == 0) (which ? v_scales : k_scales)[slot] = ok != 0.f ? scale : 0.f;
+    // Do the 4 tokens fill one quad of one block?  (The same 4 slots in every
+    // wave: uniform over the work-group.)
+    const int lo = (int)(slot & 0xffffffff), hi = (int)(slot >> 32);
+    const int64_t s0 = ((int64_t)__shfl(hi, sub, 64) << 32) | (uint32_t)__shfl(lo, sub, 64);
+    const bool quad = __all(valid && s0 % 4 == 0 && slot == s0 + e);
     uint8_t *pool = which ? v_pool : k_pool;
     const int64_t tile_bytes = (int64_t)d * BS * QBITS / 8;
-    if (valid) {
-        const int64_t blk = slot / BS;
-        const int t = (int)(slot - blk * BS);
+    const int64_t blk = valid ? slot / BS : 0;
+    const int t = valid ? (int)(slot - blk * BS) : 0;
 #pragma unroll
-        for (int i = 0; i < RC; ++i) {
-            const int c = sub + 16 * i;
-            const int h = (8 * c) / d, j = 8 * c - h * d;
-            uint8_t *tile = full ? img[which] + h * tile_bytes : pool + (blk * num_kv_heads + h) * tile_bytes;
-            int q[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) q[k] = quant_code(x[i][k], ok, scale, qmax) + (QBITS == 8 ? 128 : 8);
-            place_chunk<QBITS>(tile, which, j, t, d, q);
+    for (int i = 0; i < RC; ++i) {
+        const int c = sub + 16 * (wave + kQuadWaves * i);
+        const bool live = valid && c < nchunks;
+        const int h = (8 * c) / d, j = 8 * c - h * d;
+        uint8_t *tile = pool + (blk * num_kv_heads + h) * tile_bytes;
+        uint32_t w0, w1;
+        quant_chunk<QBITS>(x[i], ok, scale, inv, w0, w1);
+        if (which == 0 || !quad) {  // uniform per wave
+            if (live) place_chunk<QBITS>(tile, which, j, t, d, w0, w1);
+            continue;
         }
-    }
-    if (full) {  // uniform over the work-group
-        __syncthreads();
-        const int64_t units = num_kv_heads * tile_bytes / 16;
-        uint4 *dst = reinterpret_cast<uint4 *>(pool + (slot0 / BS) * num_kv_heads * tile_bytes);
-        const uint4 *from = reinterpret_cast<const uint4 *>(img[which]);
-        for (int64_t u = lt; u < units; u += 256) dst[u] = from[u];
+        const int VG = QBITS == 8 ? 4 : (d % 128 == 0 ? 8 : 4);
+        const int VLANE = VG * QBITS / 2;
+        const int vq = j / (16 * VG), vn = (j % (16 * VG)) / VG, vk = j % VG;
+        uint8_t *vbase = tile + ((int64_t)(vq * 4 + t / 4) * 16 + vn) * VLANE;  // the quad's word 0
+        if constexpr (QBITS == 8) {
+            // Words: dims 0..3 and 4..7 of the chunk; lane e stores dims e and 4 + e.
+            const uint32_t r0 = quad_transpose(w0, e, sub), r1 = quad_transpose(w1, e, sub);
+            if (live) {
+                *reinterpret_cast<uint32_t *>(vbase + e * 4) = r0;
+                *reinterpret_cast<uint32_t *>(vbase + VLANE + e * 4) = r1;
+            }
+        } else {
+            // Word: byte m = dims 2m, 2m + 1 of the token; lane e stores dim pair e.
+            const uint32_t r = quad_transpose(w0, e, sub);
+            const int jj = vk + 2 * e;
+            if (live) *reinterpret_cast<uint32_t *>(vbase + (jj / VG) * VLANE + ((jj % VG) / 2) * 4) = r;
+        }
     }
 }
 
@@ -478,13 +580,12 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
         return dlmk::fail(DLMK_ERR_INVALID_ARG,
                           "dlmk_kv_append_quant: k_src / v_src not 16-byte aligned");
     const int nc = chunks_per_lane <= 1 ? 1 : chunks_per_lane <= 2 ? 2 : chunks_per_lane <= 4 ? 4 : 8;
-    // Runs of 16 tokens per work-group for prefill-sized int8 appends with
-    // kv_dim 512 or 1024 (4 or 8 chunks per lane): config 3's 2096 tokens
-    // 12.36 -> 11.56 us.  int4 measured slower that way (8.55 -> 11.59 us)
-    // and keeps one work-group per token.
-    const int rc = quant == DLMK_I8 && n_tok >= kQuantRunMinTokens &&
-                           (kv_dim == 512 || kv_dim == kQuantRunMaxKvDim)
-                       ? (int)(kv_dim / 8 / 16) : 0;
+    // Token quads (quad kernel) for appends of kQuadMinTokens or more; else
+    // one work-group of 256 threads per token.
+    const int64_t lane_chunks = dlmk::ceil_div(kv_dim / 8, (int64_t)(16 * kQuadWaves));
+    const int rc = n_tok >= kQuadMinTokens && lane_chunks <= 8
+                       ? (lane_chunks <= 1 ? 1 : lane_chunks <= 2 ? 2 : lane_chunks <= 4 ? 4 : 8)
+                       : 0;
     const int64_t gx = n_tok;
     if (gx > 0x7fffffff) return dlmk::fail(DLMK_ERR_UNSUPPORTED, "dlmk_kv_append_quant: grid too large");
     auto s = (hipStream_t)stream;
@@ -494,24 +595,25 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
     hipLaunchKernelGGL((kv_append_quant_kernel<Q, S, NC>), dim3((unsigned)gx), dim3(256), 0, s, kp, \
                        vp, k_scales, v_scales, (const S *)k_src, (const S *)v_src, slot_mapping,  \
                        n_tok, num_kv_heads, head_dim, num_slots)
-#define DLMK_LAUNCH_RUN(Q, S, RC)                                                                    \
-    hipLaunchKernelGGL((kv_append_quant_run_kernel<Q, S, RC>), dim3((unsigned)dlmk::ceil_div(n_tok, (int64_t)16)), \
-                       dim3(512), 0, s, kp, vp, k_scales, v_scales, (const S *)k_src, (const S *)v_src,         \
-                       slot_mapping, n_tok, num_kv_heads, head_dim, num_slots)
+#define DLMK_LAUNCH_QUAD(Q, S, RC)                                                                   \
+    hipLaunchKernelGGL((kv_append_quant_quad_kernel<Q, S, RC>),                                      \
+                       dim3((unsigned)dlmk::ceil_div(n_tok, (int64_t)4), 2), dim3(64 * kQuadWaves), 0, s, \
+                       kp, vp,                                                                       \
+                       k_scales, v_scales, (const S *)k_src, (const S *)v_src, slot_mapping, n_tok,  \
+                       num_kv_heads, head_dim, num_slots)
 #define DLMK_LAUNCH(Q, S)                                             \
-    if (rc == 4) {                                                    \
-        DLMK_LAUNCH_RUN(Q, S, 4);                                     \
-        break;                                                        \
-    }                                                                 \
-    if (rc == 8) {                                                    \
-        DLMK_LAUNCH_RUN(Q, S, 8);                                     \
-        break;                                                        \
-    }                                                                 \
-    switch (nc) {                                                     \
-        case 1: DLMK_LAUNCH_NC(Q, S, 1); break;                       \
-        case 2: DLMK_LAUNCH_NC(Q, S, 2); break;                       \
-        case 4: DLMK_LAUNCH_NC(Q, S, 4); break;                       \
-        default: DLMK_LAUNCH_NC(Q, S, 8); break;                      \
+    switch (rc) {                                                     \
+        case 1: DLMK_LAUNCH_QUAD(Q, S, 1); break;                     \
+        case 2: DLMK_LAUNCH_QUAD(Q, S, 2); break;                     \
+        case 4: DLMK_LAUNCH_QUAD(Q, S, 4); break;                     \
+        case 8: DLMK_LAUNCH_QUAD(Q, S, 8); break;                     \
+        default:                                                      \
+            switch (nc) {                                             \
+                case 1: DLMK_LAUNCH_NC(Q, S, 1); break;               \
+                case 2: DLMK_LAUNCH_NC(Q, S, 2); break;               \
+                case 4: DLMK_LAUNCH_NC(Q, S, 4); break;               \
+                default: DLMK_LAUNCH_NC(Q, S, 8); break;              \
+            }                                                         \
     }
     const int q = quant == DLMK_I8 ? 8 : 4;
     switch (src_dtype * 16 + q) {
@@ -526,7 +628,7 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
                               src_dtype);
     }
 #undef DLMK_LAUNCH_NC
-#undef DLMK_LAUNCH_RUN
+#undef DLMK_LAUNCH_QUAD
 #undef DLMK_LAUNCH
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return dlmk::fail((int)e, "dlmk_kv_append_quant launch: %s", hipGetErrorString(e));

@@ -55,6 +55,25 @@ def tokens(rng, n, Hkv, d, outliers=True):
     return x
 
 
+def halfway_rows(rng, x, rows, qmax):
+    """Tokens whose quotients x / scale sit on or within a few ulps of the
+    half-integers, where the append's reciprocal-multiply rounding test must
+    fall back to the division (scale = max / qmax, with the max in element 0)."""
+    for r in rows:
+        flat = x[r].reshape(-1)
+        mx = np.float32(rng.uniform(0.5, 3.0))
+        scale = np.float32(mx / np.float32(qmax))
+        k = rng.integers(-qmax, qmax, flat.size)
+        vals = (k + 0.5).astype(np.float32) * scale
+        for step in (-2, -1, 1, 2):  # nudge some by a few ulps either way
+            sel = rng.random(flat.size) < 0.15
+            toward = np.float32(np.inf) if step > 0 else np.float32(-np.inf)
+            for _ in range(abs(step)):
+                vals[sel] = np.nextafter(vals[sel], toward)
+        vals[0] = mx
+        flat[:] = vals
+
+
 def garbage_pools(rng, oracle, nb, Hkv, d, quant):
     """Pools holding random bytes and NaN scales: slots nobody wrote."""
     ks, vs = oracle.quant_pool_shapes(nb, Hkv, d, quant)
@@ -99,11 +118,14 @@ def assert_pools_equal(kv, kp, vp, ksc, vsc, what):
     ("f16", 8, 128, 700, False),   # config-2 geometry, prefill chunk + decode tokens
     ("bf16", 2, 256, 90, False),
     ("f16", 1, 64, 33, False),     # one head, smallest head dim
-    # >= 512 tokens in sequence order: 16-token runs that fill whole blocks
-    # (tiles composed in LDS) next to runs broken by skipped slots
+    # tokens in sequence order: waves whose 4 tokens fill a block's quad
+    # (transposed V words) next to waves broken by skipped slots
     ("f16", 8, 128, 700, True),    # kv_dim 1024
     ("f32", 8, 64, 600, True),     # kv_dim 512
     ("bf16", 4, 128, 530, True),   # kv_dim 512, ragged last run
+    ("f32", 2, 64, 80, True),      # kv_dim 128: one chunk per lane
+    ("f32", 4, 64, 130, True),     # kv_dim 256
+    ("f16", 16, 64, 66, True),     # kv_dim 1024 at d 64 (int4: 4-dim V lane groups)
 ])
 def test_kv_append_quant_bit_exact(oracle, torch_mod, ops, cuda, qname, src, Hkv, d, ntok, ordered):
     torch = torch_mod
@@ -117,10 +139,19 @@ def test_kv_append_quant_bit_exact(oracle, torch_mod, ops, cuda, qname, src, Hkv
     slots[5] = nb * BS + 3                # out-of-pool slot: skipped
     k = tokens(rng, ntok, Hkv, d)
     v = tokens(rng, ntok, Hkv, d)
-    k[3] = 0.0                            # all-zero token: scale 0, codes 0
-    v[4] = 0.0
-    k[6, 0, 1] = np.nan                   # NaN element: skipped by the max, code 0
-    v[7, 0, 2] = np.inf                   # inf element: scale inf, every code 0
+    qmax = 127 if qname == "int8" else 7
+    halfway_rows(rng, k, [10, 11], qmax)
+    halfway_rows(rng, v, [12, 13], qmax)
+    for base in ((0, 32) if ntok >= 64 else (0,)):
+        # Also inside the run of tokens 32..47, which fills a whole block when
+        # ordered (no skipped or out-of-pool slot there).
+        k[base + 3] = 0.0                 # all-zero token: scale 0, codes 0
+        v[base + 4] = 0.0
+        k[base + 6, 0, 1] = np.nan        # NaN element: skipped by the max, code 0
+        v[base + 7, 0, 2] = np.inf        # inf element: scale inf, every code 0
+        if base:
+            halfway_rows(rng, k, [base + 8], qmax)
+            halfway_rows(rng, v, [base + 9], qmax)
     kd, kf = src_dev(torch, k, src, cuda)
     vd, vf = src_dev(torch, v, src, cuda)
     kp, vp, ksc, vsc = garbage_pools(rng, oracle, nb, Hkv, d, quant)
