@@ -220,19 +220,20 @@ __device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][D],
 __device__ __forceinline__ int wave_block(int b, int nb) { return DLMK_MFMA_REV ? nb - 1 - b : b; }
 
 // Fused decode step, append work-group: threads tid, tid + nthreads, ...
-// store the K and V of sequence seq's newest nq positions for kv head kvh
-// (the bits dlmk_kv_append writes; masked or out-of-pool blocks skipped).
+// store the K and V of sequence seq's newest nq positions for every kv head,
+// (kv head, position, dim) flattened over the threads (the bits
+// dlmk_kv_append writes; masked or out-of-pool blocks skipped).
 template <typename T, int D>
 __device__ __forceinline__ void append_new_tokens(T *k_pool, T *v_pool, const T *k_new,
                                                   const T *v_new, const int32_t *block_tables,
-                                                  const int32_t *ctx_lens, int seq, int kvh,
+                                                  const int32_t *ctx_lens, int seq,
                                                   int num_kv_heads, int nq, int max_blocks,
                                                   int64_t num_blocks, int tid, int nthreads) {
     constexpr int X = 16 / sizeof(T);
     constexpr int TILE = D * kBlock;
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
-    for (int e = tid; e < nq * D; e += nthreads) {
-        const int j = e / D, dim = e % D, p = ctx - nq + j;
+    for (int e = tid; e < num_kv_heads * nq * D; e += nthreads) {
+        const int dim = e % D, j = (e / D) % nq, kvh = e / (D * nq), p = ctx - nq + j;
         if (p < 0) continue;
         const int64_t blk = block_tables[(int64_t)seq * max_blocks + p / kBlock];
         if (blk < 0 || blk >= num_blocks) continue;
@@ -328,6 +329,7 @@ __device__ __forceinline__ f16x4 biased4(uint32_t w) {
 //     kBias + code (the kernel removes the bias).
 template <typename E, int D>
 struct CodecFloat {  // f16 / bf16 pools: K [d/8][16][8], V [d][16] elements
+    static constexpr int kCodeBits = 16;
     using QT = E;
     using Op = Mfma<E>;
     using KRaw = typename Op::x8;
@@ -365,6 +367,7 @@ using CodecBF16 = CodecFloat<__bf16, D>;
 //     of its quarter.
 template <int D>
 struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
+    static constexpr int kCodeBits = 8;
     using QT = _Float16;
     using Op = Mfma<_Float16>;
     using KRaw = u32x4;
@@ -392,6 +395,7 @@ struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
 
 template <int D>
 struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 64: 8-byte loads, a whole tile)
+    static constexpr int kCodeBits = 4;
     static constexpr bool kWide = D % 128 == 0;
     static constexpr int KG = kWide ? 32 : 16, VG = kWide ? 8 : 4;
     using QT = _Float16;
@@ -472,22 +476,27 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     // peak over first-index-first at the 8B shape).
     if constexpr (!C::kScaled) {
         // Fused decode step: the first row of the grid (dealt first) stores
-        // each (sequence, kv head)'s new tokens; the partition work-groups
+        // the new tokens, one work-group per sequence (the row's work-groups
+        // of kv head 0) covering all its kv heads; the partition work-groups
         // take them from k_new / v_new in registers instead of the pools.
-        // Issued at the head of the grid, the stores overlap the ramp of the
-        // read stream: 104.4 us a step at the 8B shape against 109.8 with the
-        // stores issued by the partition waves themselves (attention alone:
-        // 100.4 us).
+        // Measured at the 8B shape (configs[1], step / attention alone):
+        //   stores issued by the partition waves themselves, behind a fence:
+        //     109.8 / 100.4 us; from the owning wave's substitution
+        //     registers, no fence: 108.6 / 100.5 us;
+        //   append row, one work-group per (sequence, kv head): 105.2 / 100.7;
+        //   the same row as the grid's last (dealt last): 105.6 / 100.7;
+        //   one work-group per sequence: 103.9-104.4 / 100.7-101.0;
+        //   per 4 or 16 sequences: 107.6 / 111.1 us.
         if (k_new != nullptr && blockIdx.y == 0) {
-            append_new_tokens<QT, D>(reinterpret_cast<QT *>(k_pool), reinterpret_cast<QT *>(v_pool),
-                                     k_new, v_new, block_tables, ctx_lens, blockIdx.x / num_kv_heads,
-                                     blockIdx.x % num_kv_heads, num_kv_heads, NQ, max_blocks,
-                                     num_blocks, threadIdx.x, NW * 64);
+            if (blockIdx.x % num_kv_heads == 0)
+                append_new_tokens<QT, D>(reinterpret_cast<QT *>(k_pool), reinterpret_cast<QT *>(v_pool),
+                                         k_new, v_new, block_tables, ctx_lens, blockIdx.x / num_kv_heads,
+                                         num_kv_heads, NQ, max_blocks, num_blocks, threadIdx.x, NW * 64);
             return;
         }
     }
-    const int part = gridDim.y - 1 - blockIdx.y, kvh = blockIdx.x % num_kv_heads,
-              seq = blockIdx.x / num_kv_heads;
+    const int part = gridDim.y - 1 - blockIdx.y;
+    const int kvh = blockIdx.x % num_kv_heads, seq = blockIdx.x / num_kv_heads;
     // A length beyond the table width is clamped: no read past a table row and
     // no partition index past max_parts.
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
@@ -875,19 +884,20 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_generic_kernel(
     const int seq = blockIdx.x / geo.n_rg / num_kv_heads;
 
     if (FUSED && blockIdx.y == 0) {
-        // Fused decode step: the first grid row stores the new tokens (once
-        // per (sequence, kv head): row group 0); the partition work-groups
+        // Fused decode step: the first grid row stores the new tokens, one
+        // work-group per sequence (row group 0 of kv head 0) over all kv
+        // heads, as paged_attn_mfma_kernel; the partition work-groups
         // substitute them from k_new / v_new.
-        if (rg == 0) {
+        if (rg == 0 && kvh == 0) {
             const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
-            for (int e = threadIdx.x; e < nq * hd; e += NW * 64) {
-                const int j = e / hd, dim = e % hd, p = ctx - nq + j;
+            for (int e = threadIdx.x; e < num_kv_heads * nq * hd; e += NW * 64) {
+                const int dim = e % hd, j = (e / hd) % nq, h = e / (hd * nq), p = ctx - nq + j;
                 if (p < 0) continue;
                 const int64_t blk = block_tables[(int64_t)seq * max_blocks + p / kBlock];
                 if (blk < 0 || blk >= num_blocks) continue;
                 const int t = p % kBlock;
-                const int64_t base = (blk * num_kv_heads + kvh) * tile;
-                const int64_t src = ((int64_t)(seq * nq + j) * num_kv_heads + kvh) * hd + dim;
+                const int64_t base = (blk * num_kv_heads + h) * tile;
+                const int64_t src = ((int64_t)(seq * nq + j) * num_kv_heads + h) * hd + dim;
                 pool_store(&k_pool[base + (dim / X * kBlock + t) * X + dim % X], k_new[src]);
                 pool_store(&v_pool[base + dim * kBlock + t], v_new[src]);
             }
@@ -1366,9 +1376,9 @@ int launch_pair(const Args &a, int partition, int64_t grid_x, Launch launch) {
 }
 
 // Matrix-core path: NW waves x NB blocks per partition, pool format C.
-template <typename C, int D, int GQA, int NQ>
-int launch_mfma(const Args &a) {
-    constexpr int NW = DLMK_MFMA_NW, NB = DLMK_MFMA_NB;
+template <typename C, int D, int GQA, int NQ, int NB>
+int launch_mfma_nb(const Args &a) {
+    constexpr int NW = DLMK_MFMA_NW;
     constexpr int PD = C::kScaled ? DLMK_MFMA_PDQ : DLMK_MFMA_PD;
     static_assert(NW * NB * kBlock >= kMinPartition, "partition below the workspace bound");
     using QT = typename C::QT;
@@ -1383,6 +1393,27 @@ int launch_mfma(const Args &a) {
                            static_cast<const QT *>(a.v_new), a.tables, a.ctx_lens, a.Hq, a.Hkv,
                            a.max_blocks, a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
     });
+}
+
+// Partition shape per launch.  f16 / bf16 and int8 pools: 16 blocks per wave
+// (1024-token partitions).  int4 pools: 8 blocks per wave (512-token
+// partitions) when every row then fits the one-wave combine (max_blocks * 16
+// <= 8 x 512 tokens: configs[1] and shorter), else 16 (long rows: configs[3],
+// whose 64 partitions of 512 tokens lost 2 points to 32 of 1024).  Measured
+// at configs[1], attention only, two runs each: int4 42.5 / 41.6% of HBM peak
+// with 8 blocks against 40.7 / 40.9% with 16; int8 60.9 / 60.9% with 8
+// against 61.6 / 61.5% with 16.
+#ifndef DLMK_MFMA_QNB_SHORT
+#define DLMK_MFMA_QNB_SHORT 8
+#endif
+template <typename C, int D, int GQA, int NQ>
+int launch_mfma(const Args &a) {
+    if constexpr (C::kScaled && C::kCodeBits == 4 && DLMK_MFMA_QNB_SHORT != DLMK_MFMA_NB) {
+        constexpr int NBS = DLMK_MFMA_QNB_SHORT;
+        if (parts_for(a.max_blocks, DLMK_MFMA_NW * NBS * kBlock) <= kCombineBatch)
+            return launch_mfma_nb<C, D, GQA, NQ, NBS>(a);
+    }
+    return launch_mfma_nb<C, D, GQA, NQ, DLMK_MFMA_NB>(a);
 }
 
 // Generic kernel, NB blocks per wave (FUSED: with the fused step's append).
