@@ -78,9 +78,12 @@ def parse():
     p.add_argument("--steps", type=int, default=200, help="timed steps (rounded to a multiple of 20)")
     p.add_argument("--warmup", type=int, default=500,
                    help="untimed steps run before each timed region (lets clocks settle)")
-    p.add_argument("--workload", default="config2", choices=sorted(WORKLOADS) + ["block8b"],
+    p.add_argument("--workload", default="config2",
+                   choices=sorted(WORKLOADS) + ["block8b", "blockmoves"],
                    help="block8b: dlmk_decode_block_paged on Llama-3-8B layers (the caller "
-                        "of the paged path; a design-notes line, not the headline metric)")
+                        "of the paged path; a design-notes line, not the headline metric); "
+                        "blockmoves: block copy / gather / scatter at several sizes with a "
+                        "fixed-cost fit")
     p.add_argument("--kv-quant", default="none", choices=["none", "int8", "int4"],
                    help="store K/V as per-token-scaled int8/int4 codes (dlm's --kv-quant); "
                         "queries and new tokens stay f16")
@@ -273,6 +276,74 @@ def bench_block(args):
     }), flush=True)
 
 
+def bench_block_moves(args):
+    """dlmk_copy_blocks / dlmk_gather_blocks / dlmk_scatter_blocks on 8B-shaped
+    f16 blocks (8 kv heads x 16 tokens x 128 dims: 32 KiB per pool) at 128 ..
+    8192 blocks drawn at random from a 40,000-block pool, each size timed as
+    HIP-graph replays of 10 launches.  Bytes per launch: every block read and
+    written once in each of the K and V pools (4 x blocks x 32 KiB).  A
+    least-squares fit t = a + bytes / BW over the sizes separates a fixed
+    per-launch cost a from the streaming rate BW."""
+    import torch
+    from dlm_amd import ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    nb, bb = 40000, 8 * BS * 128 * 2
+    k = torch.zeros(nb * bb, dtype=torch.uint8, device=dev)
+    v = torch.zeros_like(k)
+    rng = np.random.default_rng(SEED)
+    sizes = [128, 512, 2048, 8192]
+    reps = 10
+    out = {}
+    for n in sizes:
+        perm = rng.permutation(nb).astype(np.int32)
+        pairs = torch.from_numpy(np.stack([perm[:n], perm[n:2 * n]], 1).copy()).to(dev)
+        ids = torch.from_numpy(perm[:n].copy()).to(dev)
+        staging = torch.empty(2 * n * bb, dtype=torch.uint8, device=dev)
+        fns = {"copy": lambda: ops.copy_blocks(k, v, pairs, bb),
+               "gather": lambda: ops.gather_blocks(k, v, ids, bb, staging),
+               "scatter": lambda: ops.scatter_blocks(k, v, staging, ids, bb)}
+        for name, fn in fns.items():
+            fn()
+            torch.cuda.synchronize()
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                for _ in range(reps):
+                    fn()
+            torch.cuda.synchronize()
+            for _ in range(3):
+                g.replay()
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            a.record()
+            for _ in range(max(1, args.steps // reps)):
+                g.replay()
+            b.record()
+            torch.cuda.synchronize()
+            us = a.elapsed_time(b) * 1e3 / (reps * max(1, args.steps // reps))
+            nbytes = 4 * n * bb
+            out.setdefault(name, []).append({"blocks": n, "bytes": nbytes, "us": round(us, 2),
+                                             "GBps": round(nbytes / (us * 1e-6) / 1e9, 1)})
+    fits = {}
+    for name, rows in out.items():
+        x = np.array([r["bytes"] for r in rows], np.float64)
+        t = np.array([r["us"] for r in rows], np.float64)
+        slope, icpt = np.polyfit(x, t, 1)
+        resid = t - (icpt + slope * x)
+        fits[name] = {"fixed_us": round(float(icpt), 2),
+                      "stream_GBps": round(float(1e-3 / slope), 1) if slope > 0 else None,
+                      "max_resid_us": round(float(np.abs(resid).max()), 2)}
+    print(json.dumps({"metric": "block move HBM GB/s by size (8B-shaped f16 blocks)",
+                      "unit": "GB/s", "n_gpus": 1, "higher_is_better": True,
+                      "data": "synthetic (zero pools, random block ids, seeded)",
+                      "config": {"workload": "blockmoves", "block_bytes_per_pool": bb,
+                                 "pool_blocks": nb, "sizes": sizes},
+                      "moves": out, "fit": fits,
+                      "timing": f"HIP events around replays of a HIP graph of {reps} launches"}),
+          flush=True)
+
+
 def copy_calibration(torch, ops, steps):
     """A plain copy of known size: 4096 pairs of 32 KiB blocks in each of the K and V pools."""
     dev = torch.device("cuda:0")
@@ -412,6 +483,9 @@ def main():
 
     if args.workload == "block8b":
         bench_block(args)
+        return
+    if args.workload == "blockmoves":
+        bench_block_moves(args)
         return
     traffic, traffic_note = None, None
     if args.traffic == "pmc" and not args.copy_calibration and args.only is None:
