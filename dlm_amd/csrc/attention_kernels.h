@@ -486,7 +486,12 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         //   append row, one work-group per (sequence, kv head): 105.2 / 100.7;
         //   the same row as the grid's last (dealt last): 105.6 / 100.7;
         //   one work-group per sequence: 103.9-104.4 / 100.7-101.0;
-        //   per 4 or 16 sequences: 107.6 / 111.1 us.
+        //   per 4 or 16 sequences: 107.6 / 111.1 us;
+        //   whole 32-byte sectors rewritten (read, substitute, store by lane
+        //   pairs), not the tokens' 2-byte elements: 112.0 against 103.5 us.
+        // With the row's stores skipped (wrong results, timing only) the step
+        // takes 100.6 us and without the substitution 103.1: the 2.7 us left
+        // over the attention is the stores themselves.
         if (k_new != nullptr && blockIdx.y == 0) {
             if (blockIdx.x % num_kv_heads == 0)
                 append_new_tokens<QT, D>(reinterpret_cast<QT *>(k_pool), reinterpret_cast<QT *>(v_pool),
