@@ -221,3 +221,81 @@ class SpeculativeDecoder:
 
     def acceptance_rate(self) -> float:
         return 0.0 if self.proposed == 0 else self.accepted / self.proposed
+
+
+class SpeculativeScheduler:
+    """``BatchScheduler::with_speculative`` (src/batching.rs:189-401): at most
+    ``max_batch`` requests in flight, each a ``SpeculativeSession`` advanced by
+    one round per tick; a round's tokens are emitted in order and the request
+    stops at its length cap or at an EOS token (inclusive), discarding the
+    rest of that round, as plain decoding would have stopped there
+    (batching.rs:337-378).  Finished requests release their blocks."""
+
+    def __init__(self, target: PagedGenerator, draft: PagedGenerator, max_batch: int,
+                 gamma: int):
+        self.target, self.draft = target, draft
+        self.max_batch = max(int(max_batch), 1)
+        self.gamma = max(int(gamma), 1)
+        self.pending: List[tuple] = []
+        self.active: List[dict] = []
+        self.proposed = self.accepted = 0
+
+    def submit(self, req_id: int, prompt: Sequence[int], max_new_tokens: int,
+               eos: Sequence[int] = ()) -> None:
+        if not prompt:
+            raise ValueError("prompt must be non-empty")
+        self.pending.append((req_id, list(prompt), int(max_new_tokens), list(eos)))
+
+    def speculative_stats(self):
+        """(proposed, accepted) over every finished request."""
+        return self.proposed, self.accepted
+
+    def has_work(self) -> bool:
+        return bool(self.pending or self.active)
+
+    def _admit(self) -> List[int]:
+        zero = []
+        while len(self.active) < self.max_batch and self.pending:
+            req_id, prompt, n, eos = self.pending.pop(0)
+            if n == 0:
+                zero.append(req_id)
+                continue
+            self.active.append({"id": req_id, "eos": eos, "remaining": n,
+                                "session": SpeculativeSession(self.target, self.draft,
+                                                              self.gamma, prompt)})
+        return zero
+
+    def step(self):
+        """One tick: returns (produced [(id, token)], finished ids)."""
+        finished = self._admit()
+        produced = []
+        still = []
+        for a in self.active:
+            s = a["session"]
+            done = False
+            for tok in s.step(a["remaining"]):
+                produced.append((a["id"], tok))
+                a["remaining"] -= 1
+                if a["remaining"] == 0 or tok in a["eos"]:
+                    done = True
+                    break
+            if done:
+                self.proposed += s.proposed
+                self.accepted += s.accepted
+                s.close()
+                finished.append(a["id"])
+            else:
+                still.append(a)
+        self.active = still
+        return produced, finished
+
+    def run(self):
+        """Ticks until every request completes: [(id, tokens)] in completion order."""
+        outputs, results = {}, []
+        while self.has_work():
+            produced, finished = self.step()
+            for req_id, tok in produced:
+                outputs.setdefault(req_id, []).append(tok)
+            for req_id in finished:
+                results.append((req_id, outputs.pop(req_id, [])))
+        return results

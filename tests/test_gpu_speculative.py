@@ -10,9 +10,10 @@ Speculative rounds (dlm_amd.speculative) over the paged path against
 target-greedy decoding computed by the oracle, with the reference's own test
 models (tests/speculative.rs:29-64: 1 layer, hidden 16, 4/2 heads, head_dim
 4, inter 32, vocab 32, SplitMix64 weights * 0.05, unit norms, target seed 1,
-draft seed 2) and its three properties (speculative.rs:77-131): output ==
-target greedy, an identical draft is fully accepted, round-by-round sessions
-respect the budget.  A 2-layer head_dim-64 model with a perturbed draft adds
+draft seed 2) and its properties (speculative.rs:77-171): output == target
+greedy, an identical draft is fully accepted, round-by-round sessions respect
+the budget, the scheduler (max_batch 2, staggered admission) matches greedy
+per request and stops at EOS.  A 2-layer head_dim-64 model with a perturbed draft adds
 mixed acceptance and rollbacks across block boundaries.
 """
 import numpy as np
@@ -248,3 +249,38 @@ def test_speculative_session_rounds_with_rollback(oracle, cuda):
                f"acceptance {s.accepted}/{s.proposed}")
         s.close()
     assert target.cache.free_blocks() == target.cache.total_blocks()
+
+
+def test_speculative_scheduler_reference_models(oracle, cuda):
+    """tests/speculative.rs:133-171 on the reference's models over the paged
+    path: max_batch 2 forces staggered admission while speculating, every
+    request equals its target greedy; then an identical draft stops at EOS
+    (included), as plain decoding does."""
+    import torch
+    from dlm_amd.speculative import SpeculativeScheduler
+    banner("speculative scheduler: reference models")
+    shape, t_layers = reference_model(oracle, 1)
+    _, d_layers = reference_model(oracle, 2)
+    target = gpu_generator(torch, cuda, shape, t_layers, 8, 24, seed=31)
+    draft = gpu_generator(torch, cuda, shape, d_layers, 8, 24, seed=32)
+    reqs = [(1, [1, 2, 3], 7), (2, [7], 5), (3, [4, 5], 6)]
+    sched = SpeculativeScheduler(target, draft, 2, 4)
+    for rid, prompt, n in reqs:
+        sched.submit(rid, prompt, n)
+    results = dict(sched.run())
+    assert set(results) == {1, 2, 3}
+    for rid, prompt, n in reqs:
+        ref, gap = oracle_greedy(oracle, shape, t_layers, prompt, n)
+        assert gap > 1e-6
+        assert results[rid] == ref, f"request {rid} diverged"
+    proposed, accepted = sched.speculative_stats()
+    assert proposed > 0 and accepted <= proposed
+    # EOS: the token plain decoding emits second (speculative.rs:157-171).
+    same = gpu_generator(torch, cuda, shape, t_layers, 8, 24, seed=33)
+    two, _ = oracle_greedy(oracle, shape, t_layers, [1, 2], 2)
+    sched = SpeculativeScheduler(target, same, 4, 4)
+    sched.submit(1, [1, 2], 10, [two[1]])
+    (rid, toks), = sched.run()
+    assert rid == 1 and toks[-1] == two[1] and toks == two[:len(toks)]
+    for g in (target, draft, same):
+        assert g.cache.num_sequences() == 0

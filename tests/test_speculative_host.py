@@ -129,3 +129,38 @@ def test_rmsnorm_and_argmax_follow_the_reference():
     assert argmax(np.array([1.0, 3.0, 3.0, 2.0], np.float32)) == 1
     assert argmax(np.array([np.nan, 1.0, 0.5], np.float32)) == 1
     assert argmax(np.array([-np.inf, -np.inf], np.float32)) == 0
+
+
+def test_scheduler_matches_greedy_across_requests():
+    """tests/speculative.rs:133-155: max_batch 2 forces staggered admission;
+    every request equals its own target greedy; stats add up."""
+    from dlm_amd.speculative import SpeculativeScheduler
+    target = HashGenerator(1)
+    draft = HashGenerator(2, agree_with=target, agree=0.7)
+    reqs = [(1, [1, 2, 3], 7), (2, [7], 5), (3, [4, 5], 6), (4, [9, 9, 9, 9], 0)]
+    sched = SpeculativeScheduler(target, draft, 2, 4)
+    for rid, prompt, n in reqs:
+        sched.submit(rid, prompt, n)
+    results = dict(sched.run())
+    assert set(results) == {1, 2, 3, 4}
+    for rid, prompt, n in reqs:
+        assert results[rid] == target.greedy(prompt, n), rid
+    proposed, accepted = sched.speculative_stats()
+    assert 0 < proposed and accepted <= proposed
+    assert target.cache.num_sequences() == 0 and draft.cache.num_sequences() == 0
+
+
+def test_scheduler_respects_eos():
+    """tests/speculative.rs:157-171: stop at EOS (included) before the cap,
+    matching plain decoding, even mid-round."""
+    from dlm_amd.speculative import SpeculativeScheduler
+    target = HashGenerator(1)
+    draft = HashGenerator(1)  # identical draft: full rounds
+    plain = target.greedy([1, 2], 10)
+    eos = plain[2]  # first reached mid-way through the first 5-token round
+    assert eos not in plain[:2]
+    sched = SpeculativeScheduler(target, draft, 4, 4)
+    sched.submit(1, [1, 2], 10, [eos])
+    (rid, toks), = sched.run()
+    assert rid == 1 and toks == plain[:3]
+    assert target.cache.num_sequences() == 0
