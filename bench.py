@@ -96,6 +96,9 @@ def parse():
                    help="pmc: measure the attention launch's HBM bytes with rocprofv3 --pmc "
                         "(FETCH_SIZE and WRITE_SIZE passes over this script, scaled by the "
                         "same counters on --copy-calibration) before the timed run")
+    p.add_argument("--verify-tokens", type=int, default=5,
+                   help="block8b: also time dlmk_verify_block_paged over this many tokens "
+                        "(a speculative round's gamma + 1; 0 skips it)")
     p.add_argument("--copy-calibration", action="store_true",
                    help="only run dlmk_copy_blocks over 4096 pairs of 32-KiB blocks in each of 2 "
                         "pools (256 MiB read + 256 MiB written per launch), to scale "
@@ -256,6 +259,39 @@ def bench_block(args):
     b.record()
     torch.cuda.synchronize()
     ms_token = a.elapsed_time(b) / (n * reps)
+
+    verify = None
+    nv = args.verify_tokens
+    if nv > 0:
+        # gamma + 1 tokens at positions ctx .. ctx + nv - 1 through both layers
+        # in one pass (the batched target verify of a speculative round).
+        xv = torch.randn((nv, H), generator=gen, device=dev)
+
+        def verify_round():
+            for layer in range(L):
+                kern.run_tokens(layer, xv, pools[layer], table_d, ctx, ctx)
+                xv.mul_(0.5)
+
+        for _ in range(3):
+            verify_round()
+        torch.cuda.synchronize()
+        gv = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(gv):
+            for _ in range(reps):
+                verify_round()
+        for _ in range(max(1, args.warmup // 50)):
+            gv.replay()
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(n):
+            gv.replay()
+        b.record()
+        torch.cuda.synchronize()
+        ms_v = a.elapsed_time(b) / (n * reps)
+        verify = {"tokens": nv, "ms_per_round": round(ms_v, 5),
+                  "us_per_layer": round(ms_v * 1e3 / L, 2),
+                  "sequential_decode_ms": round(nv * ms_token, 5),
+                  "speedup_vs_sequential": round(nv * ms_token / ms_v, 2)}
     wbytes = 2 * (cfg.q_dim * H + 2 * cfg.kv_dim * H + H * cfg.q_dim + 3 * I * H)
     kvbytes = (ctx + 1) * 2 * cfg.kv_dim * 4
     tok_bytes = L * (wbytes + kvbytes + 2 * cfg.kv_dim * 4)
@@ -272,6 +308,7 @@ def bench_block(args):
         "algorithmic_bytes_per_token": tok_bytes,
         "roofline": {"bound": "hbm", "achieved": round(gbps, 1), "peak": HBM_PEAK_GBPS,
                      "unit": "GB/s", "frac": round(gbps / HBM_PEAK_GBPS, 4)},
+        "verify": verify,
         "timing": f"HIP events around replays of a HIP graph of {reps} tokens",
     }), flush=True)
 
