@@ -52,6 +52,13 @@ int paged_attention_impl(const char *who, void *stream, void *out, int out_dtype
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: null scale pointer", who);
     if (quant && k_new)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED, "%s: no fused append into quantized pools", who);
+    // Q, the pools and the new tokens are read (and the new tokens stored) 16
+    // bytes a lane, and the scales 16 bytes a lane group.
+    const auto misaligned = [](const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 != 0; };
+    if (misaligned(q) || misaligned(k_pool) || misaligned(v_pool) || misaligned(k_new) ||
+        misaligned(v_new) || misaligned(k_scales) || misaligned(v_scales))
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "%s: q, pools, new tokens and scales must be "
+                          "16-byte aligned", who);
     if (block_size != kBlock)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED,
                           "%s: block_size %d unsupported (16)", who, block_size);

@@ -211,7 +211,9 @@ size_t dlmk_paged_attention_workspace_size(int num_seqs, int num_q_per_seq, int 
  * (>= dlmk_paged_attention_workspace_size bytes, 256-byte aligned).
  * Geometry: block_size 16; any num_q_heads / num_kv_heads group and
  * num_q_per_seq; head_dim a multiple of 4 (f32) or 8 (f16, bf16) up to 256;
- * otherwise DLMK_ERR_UNSUPPORTED. */
+ * otherwise DLMK_ERR_UNSUPPORTED.  q and the pools (and, for the step and
+ * quantized variants, the new tokens and the scales) must be 16-byte
+ * aligned, else DLMK_ERR_INVALID_ARG. */
 int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const void *q,
                                 const void *k_pool, const void *v_pool, int dtype,
                                 const int32_t *block_tables, const int32_t *ctx_lens,

@@ -57,13 +57,17 @@ def test_argument_errors_before_any_launch(dlmk):
     assert dlmk.dlmk_kv_append(None, None, None, None, None, None, 0, 8, 128, 16, 10, 1) == 0
     rc = dlmk.dlmk_copy_blocks(None, 1, 1, 1, 3, 100, 10)  # block_bytes not multiple of 16
     assert rc == _lib.DLMK_ERR_INVALID_ARG
-    rc = dlmk.dlmk_paged_decode_attention(None, 1, 1, 1, 1, 1, 1, 1, 1, 4, 1, 32, 6, 128, 16,
+    A = 4096  # a stand-in device address, 16-byte aligned (never dereferenced)
+    rc = dlmk.dlmk_paged_decode_attention(None, A, 1, A, A, A, 1, A, A, 4, 1, 32, 6, 128, 16,
                                           8, 100, 0.1, None, 0)  # 32 % 6 != 0
     assert rc == _lib.DLMK_ERR_INVALID_ARG
-    rc = dlmk.dlmk_paged_decode_attention(None, 1, 1, 1, 1, 1, 1, 1, 1, 4, 1, 32, 8, 128, 32,
+    rc = dlmk.dlmk_paged_decode_attention(None, A, 1, A + 2, A, A, 1, A, A, 4, 1, 32, 8, 128, 16,
+                                          8, 100, 0.1, None, 0)  # q 2 bytes off 16
+    assert rc == _lib.DLMK_ERR_INVALID_ARG and "aligned" in _lib.last_error()
+    rc = dlmk.dlmk_paged_decode_attention(None, A, 1, A, A, A, 1, A, A, 4, 1, 32, 8, 128, 32,
                                           8, 100, 0.1, None, 0)  # block_size 32
     assert rc == _lib.DLMK_ERR_UNSUPPORTED
-    rc = dlmk.dlmk_paged_decode_attention(None, 1, 1, 1, 1, 1, 1, 1, 1, 4, 1, 32, 8, 128, 16,
+    rc = dlmk.dlmk_paged_decode_attention(None, A, 1, A, A, A, 1, A, A, 4, 1, 32, 8, 128, 16,
                                           64, 100, 0.1, None, 0)  # needs workspace
     assert rc == _lib.DLMK_ERR_WORKSPACE
     rc = dlmk.dlmk_swap_out(None, 1, 1, 1, 1, 2, 64, 10, 1, 100)  # staging 100 < 256

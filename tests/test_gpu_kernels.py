@@ -296,6 +296,21 @@ def test_paged_attention_nan_workspace(oracle, torch_mod, ops, cuda, dtype, ctx,
     assert_close(out.cpu().numpy(), oracle_attention(oracle, w), atol, rtol, "NaN workspace")
 
 
+def test_paged_attention_rejects_misaligned_operands(torch_mod, ops, cuda):
+    """Q and the pools are read 16 bytes a lane: a view 2 bytes off the
+    allocation is refused before any launch."""
+    torch = torch_mod
+    from dlm_amd import DlmkError
+    kp = torch.zeros((4, 8, 16, 16, 8), dtype=torch.float16, device=cuda)
+    vp = torch.zeros((4, 8, 128, 16), dtype=torch.float16, device=cuda)
+    t = torch.zeros((1, 4), dtype=torch.int32, device=cuda)
+    lens = torch.ones(1, dtype=torch.int32, device=cuda)
+    q = torch.zeros(1 * 32 * 128 + 1, dtype=torch.float16, device=cuda)[1:].view(1, 1, 32, 128)
+    with pytest.raises(DlmkError):
+        ops.paged_decode_attention(q, kp, vp, t, lens, num_kv_heads=8)
+    torch.cuda.synchronize()
+
+
 def test_paged_attention_unsupported_shape_raises(torch_mod, ops, cuda):
     torch = torch_mod
     from dlm_amd import DlmkError
