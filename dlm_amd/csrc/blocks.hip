@@ -104,6 +104,8 @@ int dlmk_copy_blocks(void *stream, void *k_pool, void *v_pool, const int32_t *pa
     if (n == 0) return DLMK_OK;
     if (!k_pool || !v_pool || !pairs)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_copy_blocks: null pointer");
+    if (!dlmk::aligned16(k_pool) || !dlmk::aligned16(v_pool))
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_copy_blocks: pools and staging must be 16-byte aligned");
     hipLaunchKernelGGL(copy_blocks_kernel, dim3((unsigned)n, 2), dim3(kThreads), 0,
                        (hipStream_t)stream, (char *)k_pool, (char *)v_pool, pairs,
                        (int64_t)block_bytes, num_blocks);
@@ -117,6 +119,8 @@ int dlmk_gather_blocks(void *stream, void *staging, const void *k_pool, const vo
     if (n == 0) return DLMK_OK;
     if (!staging || !k_pool || !v_pool || !block_ids)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_gather_blocks: null pointer");
+    if (!dlmk::aligned16(staging) || !dlmk::aligned16(k_pool) || !dlmk::aligned16(v_pool))
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_gather_blocks: pools and staging must be 16-byte aligned");
     hipLaunchKernelGGL(gather_blocks_kernel, dim3((unsigned)n, 2), dim3(kThreads), 0,
                        (hipStream_t)stream, (char *)staging, (const char *)k_pool,
                        (const char *)v_pool, block_ids, (int64_t)block_bytes, num_blocks);
@@ -130,6 +134,8 @@ int dlmk_scatter_blocks(void *stream, void *k_pool, void *v_pool, const void *st
     if (n == 0) return DLMK_OK;
     if (!staging || !k_pool || !v_pool || !block_ids)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_scatter_blocks: null pointer");
+    if (!dlmk::aligned16(staging) || !dlmk::aligned16(k_pool) || !dlmk::aligned16(v_pool))
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_scatter_blocks: pools and staging must be 16-byte aligned");
     hipLaunchKernelGGL(scatter_blocks_kernel, dim3((unsigned)n, 2), dim3(kThreads), 0,
                        (hipStream_t)stream, (char *)k_pool, (char *)v_pool,
                        (const char *)staging, block_ids, (int64_t)block_bytes, num_blocks);

@@ -14,4 +14,7 @@ int fail(int code, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// The kernels move 16 bytes a lane: operands must start on a 16-byte boundary.
+inline bool aligned16(const void *p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
 }  // namespace dlmk

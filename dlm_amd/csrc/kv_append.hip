@@ -366,6 +366,9 @@ extern "C" int dlmk_kv_append(void *stream, void *k_pool, void *v_pool, const vo
     if (n_tok == 0) return DLMK_OK;
     if (!k_pool || !v_pool || !k_src || !v_src || !slot_mapping)
         return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_kv_append: null pointer");
+    if (!dlmk::aligned16(k_pool) || !dlmk::aligned16(v_pool) || !dlmk::aligned16(k_src) ||
+        !dlmk::aligned16(v_src))
+        return dlmk::fail(DLMK_ERR_INVALID_ARG, "dlmk_kv_append: pools and sources must be 16-byte aligned");
     int eb;
     switch (dtype) {
         case DLMK_F32: eb = 4; break;
@@ -576,9 +579,10 @@ extern "C" int dlmk_kv_append_quant(void *stream, void *k_pool, void *v_pool, fl
     if (chunks_per_lane > 8)
         return dlmk::fail(DLMK_ERR_UNSUPPORTED,
                           "dlmk_kv_append_quant: kv_dim %lld above 8192", (long long)kv_dim);
-    if (reinterpret_cast<uintptr_t>(k_src) % 16 || reinterpret_cast<uintptr_t>(v_src) % 16)
+    if (!dlmk::aligned16(k_src) || !dlmk::aligned16(v_src) || !dlmk::aligned16(k_pool) ||
+        !dlmk::aligned16(v_pool))
         return dlmk::fail(DLMK_ERR_INVALID_ARG,
-                          "dlmk_kv_append_quant: k_src / v_src not 16-byte aligned");
+                          "dlmk_kv_append_quant: sources and pools must be 16-byte aligned");
     const int nc = chunks_per_lane <= 1 ? 1 : chunks_per_lane <= 2 ? 2 : chunks_per_lane <= 4 ? 4 : 8;
     // Token quads (quad kernel) for appends of kQuadMinTokens or more; else
     // one work-group of 256 threads per token.

@@ -185,7 +185,8 @@ int dlmk_cache_fill_block_tables(const dlmk_kv_cache *cache, const uint64_t *seq
  * KvLayerCache::append, src/forward/cpu.rs:765-795).  k_src/v_src are
  * [n_tok][num_kv_heads][head_dim]; token i goes to slot_mapping[i].  A negative
  * slot, or one >= num_blocks * block_size, is skipped.  A bit copy (f32, f16,
- * bf16).  Per-token decode and per-chunk prefill alike. */
+ * bf16).  Per-token decode and per-chunk prefill alike.  Pools and sources
+ * must be 16-byte aligned, else DLMK_ERR_INVALID_ARG. */
 int dlmk_kv_append(void *stream, void *k_pool, void *v_pool, const void *k_src,
                    const void *v_src, const int64_t *slot_mapping, int64_t n_tok,
                    int num_kv_heads, int head_dim, int block_size, int64_t num_blocks,
@@ -302,7 +303,8 @@ int dlmk_paged_decode_attention_quant(void *stream, void *out, int out_dtype, co
  * int32[n][2]) copy block src to block dst in both pools.  block_bytes is the
  * size of one block of one pool (num_kv_heads * block_size * head_dim * elem
  * bytes), a multiple of 16.  Pairs must not chain (no dst is another's src).
- * Ids outside [0, num_blocks) are skipped. */
+ * Ids outside [0, num_blocks) are skipped.  The pools (and below, the
+ * staging buffer) must be 16-byte aligned, else DLMK_ERR_INVALID_ARG. */
 int dlmk_copy_blocks(void *stream, void *k_pool, void *v_pool, const int32_t *pairs, int64_t n,
                      size_t block_bytes, int64_t num_blocks);
 

@@ -51,13 +51,17 @@ def test_argument_errors_before_any_launch(dlmk):
     assert "bad sizes" in _lib.last_error()
     rc = dlmk.dlmk_kv_append(None, None, None, None, None, None, 4, 8, 128, 16, 10, 1)
     assert rc == _lib.DLMK_ERR_INVALID_ARG
-    rc = dlmk.dlmk_kv_append(None, 1, 1, 1, 1, 1, 4, 8, 12, 16, 10, 1)  # 12*2 % 16 != 0
+    A = 4096  # a stand-in device address, 16-byte aligned (never dereferenced)
+    rc = dlmk.dlmk_kv_append(None, A, A, A, A, A, 4, 8, 12, 16, 10, 1)  # 12*2 % 16 != 0
     assert rc == _lib.DLMK_ERR_UNSUPPORTED
+    rc = dlmk.dlmk_kv_append(None, A, A, A + 4, A, A, 4, 8, 128, 16, 10, 1)  # k_src 4 bytes off
+    assert rc == _lib.DLMK_ERR_INVALID_ARG and "aligned" in _lib.last_error()
+    rc = dlmk.dlmk_copy_blocks(None, A + 8, A, A, 3, 64, 10)  # k_pool 8 bytes off
+    assert rc == _lib.DLMK_ERR_INVALID_ARG and "aligned" in _lib.last_error()
     # Zero tokens is a successful no-op.
     assert dlmk.dlmk_kv_append(None, None, None, None, None, None, 0, 8, 128, 16, 10, 1) == 0
     rc = dlmk.dlmk_copy_blocks(None, 1, 1, 1, 3, 100, 10)  # block_bytes not multiple of 16
     assert rc == _lib.DLMK_ERR_INVALID_ARG
-    A = 4096  # a stand-in device address, 16-byte aligned (never dereferenced)
     rc = dlmk.dlmk_paged_decode_attention(None, A, 1, A, A, A, 1, A, A, 4, 1, 32, 6, 128, 16,
                                           8, 100, 0.1, None, 0)  # 32 % 6 != 0
     assert rc == _lib.DLMK_ERR_INVALID_ARG
