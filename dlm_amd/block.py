@@ -215,14 +215,9 @@ class PagedGpuKernel:
             k_pool.numel() // tile, _ptr(block_table), self.max_blocks, num_positions, position,
             _ptr(self.workspace), self.workspace.numel()))
 
-    def run_tokens(self, layer: int, hidden: torch.Tensor, kv: Tuple[torch.Tensor, torch.Tensor],
-                   block_table: torch.Tensor, num_positions: int, position: int,
-                   stream=None) -> None:
-        """run_block over n consecutive tokens in one pass (the batched verify
-        of a speculative round): hidden f32 [n, hidden_size], token j at
-        position num_positions + j, attending causally."""
-        n = hidden.shape[0] if hidden.dim() == 2 else 1
-        self._check_kv(hidden, n, kv, block_table)
+    def verify_workspace(self, n: int) -> torch.Tensor:
+        """The workspace of dlmk_verify_block_paged over n tokens (allocated on
+        first use, then reused)."""
         ws = self._verify_ws.get(n)
         if ws is None:
             c = self.cfg
@@ -231,6 +226,17 @@ class PagedGpuKernel:
                 self.max_blocks, n)
             ws = self._verify_ws[n] = torch.empty(max(nbytes, 256), dtype=torch.uint8,
                                                   device=self.device)
+        return ws
+
+    def run_tokens(self, layer: int, hidden: torch.Tensor, kv: Tuple[torch.Tensor, torch.Tensor],
+                   block_table: torch.Tensor, num_positions: int, position: int,
+                   stream=None) -> None:
+        """run_block over n consecutive tokens in one pass (the batched verify
+        of a speculative round): hidden f32 [n, hidden_size], token j at
+        position num_positions + j, attending causally."""
+        n = hidden.shape[0] if hidden.dim() == 2 else 1
+        self._check_kv(hidden, n, kv, block_table)
+        ws = self.verify_workspace(n)
         k_pool, v_pool = kv
         tile = self.cfg.kv_dim * BLOCK_SIZE
         check(lib().dlmk_verify_block_paged(

@@ -80,34 +80,41 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("name,shape,w_dtype,tol,biases,rope", CASES, ids=[c[0] for c in CASES])
-def test_decode_block_matches_oracle(oracle, cuda, name, shape, w_dtype, tol, biases, rope):
+def run_case(oracle, cuda, name, shape, w_dtype, tol, biases, rope, hist=14, max_blocks=8,
+             steps=4, poison=False):
+    """Runs `steps` decode steps of two layers from a `hist`-token history on
+    shuffled blocks and checks the hidden state and the appended K/V."""
     import torch
     from dlm_amd.block import BlockConfig, PagedGpuKernel, rope_inv_freqs
 
     H, Hq, Hkv, d, I = shape
-    banner(f"decode block {name}: hidden={H} heads={Hq}/{Hkv} d={d} inter={I} w_dtype={w_dtype}")
+    banner(f"decode block {name}: hidden={H} heads={Hq}/{Hkv} d={d} inter={I} w_dtype={w_dtype} "
+           f"hist={hist}")
     cfg = BlockConfig(H, Hq, Hkv, d, I, rope_theta=rope[0], rms_eps=1e-5, rope_scaling=rope[1])
     gs = 128 if w_dtype in (W_INT4, W_INT8) else 0
     host = [make_layer(oracle, 17 + L, H, Hq, Hkv, d, I, w_dtype, biases) for L in range(2)]
     kern = PagedGpuKernel(cfg, [to_layer(torch, w, cuda) for w in host], w_dtype, gs,
-                          max_blocks_per_seq=8, device=cuda)
+                          max_blocks_per_seq=max_blocks, device=cuda)
+    if poison:  # the block must not rely on a zeroed workspace
+        kern.workspace.fill_(0x7f)
     inv = rope_inv_freqs(d, rope[0], rope[1])  # the host-side frequencies the device reads
 
-    nb, hist = 12, 14
+    used = (hist + steps + 15) // 16
+    nb = used + 9
     rng = np.random.default_rng(5)
-    table = np.full(8, 0, np.int32)
-    table[:3] = rng.permutation(nb)[:3]
+    table = np.full(max_blocks, 0, np.int32)
+    table[:used] = rng.permutation(nb)[:used]
     pools_h = []
     for L in range(2):
         kp = np.zeros((nb, Hkv, d * 16), np.float32)
         vp = np.zeros((nb, Hkv, d * 16), np.float32)
-        for p in range(hist):  # a prior history in both pools
-            k = (rng.standard_normal((1, Hkv, d)) * 0.5).astype(np.float32)
-            v = (rng.standard_normal((1, Hkv, d)) * 0.5).astype(np.float32)
-            slot = np.array([table[p // 16] * 16 + p % 16], np.int64)
-            oracle.paged_append(kp.reshape(nb, Hkv, d // 4, 16, 4), vp.reshape(nb, Hkv, d, 16),
-                                k, v, slot, Hkv, d, 16)
+        # a prior history in both pools
+        k = (rng.standard_normal((hist, Hkv, d)) * 0.5).astype(np.float32)
+        v = (rng.standard_normal((hist, Hkv, d)) * 0.5).astype(np.float32)
+        p = np.arange(hist)
+        slots = (table[p // 16].astype(np.int64) * 16 + p % 16).astype(np.int64)
+        oracle.paged_append(kp.reshape(nb, Hkv, d // 4, 16, 4), vp.reshape(nb, Hkv, d, 16),
+                            k, v, slots, Hkv, d, 16)
         pools_h.append((kp, vp))
     pools_d = [(torch.from_numpy(kp.copy()).to(cuda), torch.from_numpy(vp.copy()).to(cuda))
                for kp, vp in pools_h]
@@ -117,7 +124,7 @@ def test_decode_block_matches_oracle(oracle, cuda, name, shape, w_dtype, tol, bi
              w_dtype=w_dtype, w_group_size=gs)
     x_ref = (np.arange(H) % 17 * 0.03 - 0.25).astype(np.float32)  # gpu_parity.rs:143-145
     x_dev = torch.from_numpy(x_ref.copy()).to(cuda)
-    for step in range(4):
+    for step in range(steps):
         p = hist + step
         for L in range(2):
             x_ref = oracle.decode_block_paged(c, host[L], x_ref, pools_h[L][0], pools_h[L][1],
@@ -130,6 +137,28 @@ def test_decode_block_matches_oracle(oracle, cuda, name, shape, w_dtype, tol, bi
     for L in range(2):  # the appended K/V (after RoPE) match too
         for dev_pool, host_pool in zip(pools_d[L], pools_h[L]):
             np.testing.assert_allclose(dev_pool.cpu().numpy(), host_pool, atol=tol, rtol=0)
+
+
+@pytest.mark.parametrize("name,shape,w_dtype,tol,biases,rope", CASES, ids=[c[0] for c in CASES])
+def test_decode_block_matches_oracle(oracle, cuda, name, shape, w_dtype, tol, biases, rope):
+    run_case(oracle, cuda, name, shape, w_dtype, tol, biases, rope)
+
+
+LONG = [
+    # name, shape, w_dtype, tol, hist, max_blocks: several split-K partitions
+    # and the combine launch, on a workspace that starts as garbage
+    ("f32-hist700", (256, 4, 2, 64, 512), W_F32, 1e-3, 700, 64),
+    ("hidden2048-d128-hist1000", (2048, 16, 4, 128, 512), W_F32, 2e-3, 1000, 80),
+    ("gqa16-hist330", (1024, 16, 1, 64, 512), W_F32, 1e-3, 330, 32),
+    ("d96-gqa3-hist200", (384, 6, 2, 96, 512), W_F32, 1e-3, 200, 16),
+    ("hidden32-d8-hist150", (32, 4, 2, 8, 64), W_F32, 1e-3, 150, 16),
+]
+
+
+@pytest.mark.parametrize("name,shape,w_dtype,tol,hist,max_blocks", LONG, ids=[c[0] for c in LONG])
+def test_decode_block_long_context(oracle, cuda, name, shape, w_dtype, tol, hist, max_blocks):
+    run_case(oracle, cuda, name, shape, w_dtype, tol, False, (10000.0, None), hist=hist,
+             max_blocks=max_blocks, steps=3, poison=True)
 
 
 def test_decode_token_books_and_pools(oracle, cuda):

@@ -40,36 +40,47 @@ VERIFY_CASES = [
     ("hidden2048-n5", (2048, 16, 4, 128, 512), W_F32, 5, 2e-3),
     ("speculative-model-n5", (16, 4, 2, 4, 32), W_F32, 5, 1e-3),
     ("gpu_parity-d8-n3", (32, 4, 2, 8, 64), W_F32, 3, 1e-3),
+    # Long histories: several split-K partitions and the combine launch;
+    # gqa16 x 5 tokens is 5 row groups of 16 rows.
+    ("f32-n2-hist500", (256, 4, 2, 64, 512), W_F32, 2, 1e-3, 500, 40),
+    ("f32-n5-hist600", (256, 4, 2, 64, 512), W_F32, 5, 1e-3, 600, 48),
+    ("hidden2048-n5-hist900", (2048, 16, 4, 128, 512), W_F32, 5, 2e-3, 900, 64),
+    ("gqa16-n5-hist300", (1024, 16, 1, 64, 512), W_F32, 5, 1e-3, 300, 32),
 ]
 
 
-@pytest.mark.parametrize("name,shape,w_dtype,n,tol", VERIFY_CASES, ids=[c[0] for c in VERIFY_CASES])
-def test_verify_block_matches_sequential_oracle(oracle, cuda, name, shape, w_dtype, n, tol):
+@pytest.mark.parametrize("name,shape,w_dtype,n,tol,hist,max_blocks",
+                         [c if len(c) == 7 else c + (13, 4) for c in VERIFY_CASES],
+                         ids=[c[0] for c in VERIFY_CASES])
+def test_verify_block_matches_sequential_oracle(oracle, cuda, name, shape, w_dtype, n, tol, hist,
+                                                max_blocks):
+    """hist 13: 13 + n crosses the first block boundary for n >= 4."""
     import torch
     from dlm_amd.block import BlockConfig, PagedGpuKernel, rope_inv_freqs
 
     H, Hq, Hkv, d, I = shape
-    banner(f"verify block {name}: hidden={H} heads={Hq}/{Hkv} d={d} inter={I} n={n}")
+    banner(f"verify block {name}: hidden={H} heads={Hq}/{Hkv} d={d} inter={I} n={n} hist={hist}")
     cfg = BlockConfig(H, Hq, Hkv, d, I)
     gs = 128 if w_dtype == W_INT8 else 0
     host = [make_layer(oracle, 41 + L, H, Hq, Hkv, d, I, w_dtype) for L in range(2)]
     kern = PagedGpuKernel(cfg, [to_layer(torch, w, cuda) for w in host], w_dtype, gs,
-                          max_blocks_per_seq=4, device=cuda)
+                          max_blocks_per_seq=max_blocks, device=cuda)
     inv = rope_inv_freqs(d, 10000.0)
-    nb, hist = 10, 13  # 13 + n crosses the first block boundary for n >= 4
+    used = (hist + n + 15) // 16
+    nb = used + 7
     rng = np.random.default_rng(n)
-    table = np.zeros(4, np.int32)
-    table[:3] = rng.permutation(nb)[:3]
+    table = np.zeros(max_blocks, np.int32)
+    table[:used] = rng.permutation(nb)[:used]
     pools_h = []
     for L in range(2):
         kp = np.zeros((nb, Hkv, d * 16), np.float32)
         vp = np.zeros((nb, Hkv, d * 16), np.float32)
-        for p in range(hist):
-            k = (rng.standard_normal((1, Hkv, d)) * 0.5).astype(np.float32)
-            v = (rng.standard_normal((1, Hkv, d)) * 0.5).astype(np.float32)
-            slot = np.array([table[p // 16] * 16 + p % 16], np.int64)
-            oracle.paged_append(kp.reshape(nb, Hkv, d // 4, 16, 4), vp.reshape(nb, Hkv, d, 16),
-                                k, v, slot, Hkv, d, 16)
+        k = (rng.standard_normal((hist, Hkv, d)) * 0.5).astype(np.float32)
+        v = (rng.standard_normal((hist, Hkv, d)) * 0.5).astype(np.float32)
+        p = np.arange(hist)
+        slots = (table[p // 16].astype(np.int64) * 16 + p % 16).astype(np.int64)
+        oracle.paged_append(kp.reshape(nb, Hkv, d // 4, 16, 4), vp.reshape(nb, Hkv, d, 16),
+                            k, v, slots, Hkv, d, 16)
         pools_h.append((kp, vp))
     pools_d = [(torch.from_numpy(kp.copy()).to(cuda), torch.from_numpy(vp.copy()).to(cuda))
                for kp, vp in pools_h]
@@ -78,6 +89,7 @@ def test_verify_block_matches_sequential_oracle(oracle, cuda, name, shape, w_dty
              w_dtype=w_dtype, w_group_size=gs)
     x = (rng.uniform(-0.5, 0.5, (n, H))).astype(np.float32)
     x_dev = torch.from_numpy(x.copy()).to(cuda)
+    kern.verify_workspace(n).fill_(0x7f)  # the block must not rely on a zeroed workspace
     for L in range(2):
         kern.run_tokens(L, x_dev, pools_d[L], table_d, hist, hist)
     ref = np.empty_like(x)
