@@ -1245,9 +1245,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wave_ke
 }
 
 // Rows of more than kCombineBatch partitions: one work-group of
-// kCombineWaves waves per (query row, sequence).  Wave w loads its first
-// partition (w) before the context length arrives, folds w + W, ... in
-// batches with an online rescale, and the waves merge once in LDS.
+// kCombineWaves waves per (query row, sequence).  Wave w folds partitions
+// w, w + W, ... in batches of 8 with an online rescale (its first batch loaded
+// before the context length arrives), and the waves merge once in LDS.
 template <int DPL>
 __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
@@ -1262,44 +1262,32 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kern
     const float *ml = ws_ml + 2 * row * max_parts;
     const float *o = ws_o + row * max_parts * D;
 
-    // Wave w's first partition (w) is loaded before the context length is
-    // known (the slot exists for every w < max_parts; it is used only if
-    // w < nparts), so the common case -- at most W partitions -- costs one
-    // memory round trip.  Further partitions w + W, ... fold in with an
-    // online rescale; the W waves then merge once.
-    float m = -INFINITY, L = 0.f, O[DPL];
-    float m0 = -INFINITY, l0 = 0.f, o0[DPL];
-#pragma unroll
-    for (int k = 0; k < DPL; ++k) O[k] = o0[k] = 0.f;
-    if (wave < max_parts) {
-        m0 = ml[2 * wave];
-        l0 = ml[2 * wave + 1];
-#pragma unroll
-        for (int k = 0; k < DPL; ++k) o0[k] = o[(int64_t)wave * D + min(lane + 64 * k, D - 1)];
-    }
-    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
-    const int nparts = parts_of(ctx, partition);
-    if (nparts == 1) return;
-    if (wave < nparts) {
-        m = m0;
-        L = l0;
-#pragma unroll
-        for (int k = 0; k < DPL; ++k) O[k] = o0[k];
-    }
-    // Later partitions in batches of B per wave: all of a batch's loads go
-    // out before any is folded (indices clamped into the row, folds skipped
-    // past nparts).
+    // Wave w's first batch -- partitions w, w + W, ..., w + (B - 1) W,
+    // clamped into the row -- is loaded before the context length is known
+    // (every slot below max_parts exists; only those below nparts are
+    // folded), so rows of up to B x W partitions cost one memory round trip.
+    // Later partitions fold in further batches with an online rescale; the W
+    // waves then merge once.
     constexpr int B = 8;
-    for (int p0 = wave + W; p0 < nparts; p0 += B * W) {
-        float mb[B], lb[B], ob[B][DPL];
+    float m = -INFINITY, L = 0.f, O[DPL];
+#pragma unroll
+    for (int k = 0; k < DPL; ++k) O[k] = 0.f;
+    float mb[B], lb[B], ob[B][DPL];
+    auto load = [&](int p0, int last) {
 #pragma unroll
         for (int i = 0; i < B; ++i) {
-            const int p = min(p0 + i * W, nparts - 1);
+            const int p = min(p0 + i * W, last);
             mb[i] = ml[2 * p];
             lb[i] = ml[2 * p + 1];
 #pragma unroll
             for (int k = 0; k < DPL; ++k) ob[i][k] = o[(int64_t)p * D + min(lane + 64 * k, D - 1)];
         }
+    };
+    load(wave, max_parts - 1);
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    const int nparts = parts_of(ctx, partition);
+    if (nparts == 1) return;
+    for (int p0 = wave;;) {
 #pragma unroll
         for (int i = 0; i < B; ++i) {
             if (p0 + i * W >= nparts) break;
@@ -1312,6 +1300,9 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kern
             for (int k = 0; k < DPL; ++k) O[k] = fa * O[k] + fb * ob[i][k];
             m = mn;
         }
+        p0 += B * W;
+        if (p0 >= nparts) break;
+        load(p0, nparts - 1);
     }
 #pragma unroll
     for (int k = 0; k < DPL; ++k) so[wave][lane + 64 * k] = O[k];
