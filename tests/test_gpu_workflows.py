@@ -7,6 +7,8 @@ match the oracle over the mirror within the stated tolerance.  The oracle runs
 on reduced sizes where its cost would be minutes; size-independent properties
 (books invariants, bit-exact pools, round trips) are checked at full size.
 """
+from concurrent.futures import ThreadPoolExecutor
+
 import numpy as np
 import pytest
 
@@ -102,9 +104,15 @@ class Mirror:
         out = out.cpu().numpy()
         idx = list(range(len(seqs))) if check is None else list(check)
         if idx:
-            ref = self.oracle.paged_attention(q[idx], self.kh, self.vh, tables[idx], lens[idx], nq,
-                                              self.hq, HKV, D, BS, 1.0 / np.sqrt(D))
-            assert_close(out[idx], ref, F16_ATOL, F16_RTOL, "attention vs oracle")
+            # The oracle's C call releases the GIL: sequences in parallel.
+            groups = [idx[i::8] for i in range(min(8, len(idx)))]
+            run = lambda g: self.oracle.paged_attention(
+                q[g], self.kh, self.vh, tables[g], lens[g], nq, self.hq, HKV, D, BS,
+                1.0 / np.sqrt(D))
+            with ThreadPoolExecutor(len(groups)) as ex:
+                refs = list(ex.map(run, groups))
+            for g, ref in zip(groups, refs):
+                assert_close(out[g], ref, F16_ATOL, F16_RTOL, "attention vs oracle")
         return out
 
     def assert_pools_equal(self, ids=None):
