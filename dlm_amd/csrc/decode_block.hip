@@ -562,8 +562,9 @@ void launch_gemv_rw(hipStream_t st, const GemvArgs &a) {
     hipLaunchKernelGGL(kernel, dim3(grid), dim3(64 * kGemvWaves), lds, st, a);
 }
 
-// About 16 weight loads in flight per lane (8 per matrix for SwiGLU): rows of
-// at least 16 (8) loads per lane run one at a time, shorter rows 2 or 4 at once.
+// T weight loads in flight per lane -- 16, or 8 per matrix for SwiGLU and 8 for
+// one-token residual launches: rows of at least T loads per lane run one at a
+// time, shorter rows 2 or 4 at once.
 // Several tokens (NT > 1) do NT times the arithmetic per load and hold NT
 // accumulators per row: one row per wave (two for the RoPE pairs) and 8 (4
 // per matrix) loads in flight.  Measured on two Llama-3-8B layers, verify of
@@ -572,9 +573,17 @@ void launch_gemv_rw(hipStream_t st, const GemvArgs &a) {
 template <int DT, int EPI, int NT>
 void launch_gemv_epi(hipStream_t st, const GemvArgs &a) {
     constexpr int T0 = EPI == kSwiGLU ? 8 : 16;
-    constexpr int T = NT == 1 ? T0 : T0 / 2;
+    // One-token residual launches (o_proj, down_proj): 8 loads in flight per
+    // lane, whose registers allow more resident waves (8B layer 95.2 -> 94.1
+    // us; the verify's several-token launches keep T0 / 2).
+    constexpr int T = NT == 1 ? (EPI == kAddInto ? 8 : T0) : T0 / 2;
     if constexpr (EPI == kRopeAppend) {
-        launch_gemv_rw<DT, EPI, 2, (T / 2 > 1 ? T / 2 : 1), NT>(st, a);  // RoPE pairs: two rows per wave
+        // RoPE pairs: two rows per wave.  One token: 4 loads per row, whose
+        // registers allow 3 waves per SIMD, so the 8B layer's 6144 q/k/v rows
+        // fit one pass of resident work-groups (14.2 -> 13.1 us; 8 loads per
+        // row held 2 waves per SIMD and took 1.5 passes).
+        constexpr int UR = NT == 1 ? T / 4 : T / 2;
+        launch_gemv_rw<DT, EPI, 2, (UR > 1 ? UR : 1), NT>(st, a);
     } else if constexpr (NT > 1) {
         launch_gemv_rw<DT, EPI, 1, T, NT>(st, a);
     } else {
