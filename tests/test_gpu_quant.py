@@ -74,6 +74,22 @@ def halfway_rows(rng, x, rows, qmax):
         flat[:] = vals
 
 
+def tie_rows(rng, x, rows, qmax):
+    """Tokens whose quotients are exact half-integers (scale a power of two:
+    max = qmax / 8, so scale = 1/8 and x = (k + 1/2) / 8, exact in f16 and
+    bf16), some nudged by one f16 ulp: round half away from zero and its
+    neighbours, for every source dtype."""
+    for r in rows:
+        flat = x[r].reshape(-1)
+        k = rng.integers(-qmax, qmax, flat.size)
+        vals = ((k + 0.5) / 8.0).astype(np.float16)
+        for toward in (np.float16(np.inf), np.float16(-np.inf)):
+            sel = rng.random(flat.size) < 0.2
+            vals[sel] = np.nextafter(vals[sel], toward)
+        vals[0] = np.float16(qmax / 8.0)
+        flat[:] = vals.astype(np.float32)
+
+
 def garbage_pools(rng, oracle, nb, Hkv, d, quant):
     """Pools holding random bytes and NaN scales: slots nobody wrote."""
     ks, vs = oracle.quant_pool_shapes(nb, Hkv, d, quant)
@@ -142,6 +158,8 @@ def test_kv_append_quant_bit_exact(oracle, torch_mod, ops, cuda, qname, src, Hkv
     qmax = 127 if qname == "int8" else 7
     halfway_rows(rng, k, [10, 11], qmax)
     halfway_rows(rng, v, [12, 13], qmax)
+    tie_rows(rng, k, [14, 15], qmax)
+    tie_rows(rng, v, [16, 17], qmax)
     for base in ((0, 32) if ntok >= 64 else (0,)):
         # Also inside the run of tokens 32..47, which fills a whole block when
         # ordered (no skipped or out-of-pool slot there).
@@ -152,6 +170,8 @@ def test_kv_append_quant_bit_exact(oracle, torch_mod, ops, cuda, qname, src, Hkv
         if base:
             halfway_rows(rng, k, [base + 8], qmax)
             halfway_rows(rng, v, [base + 9], qmax)
+            tie_rows(rng, k, [base + 10], qmax)
+            tie_rows(rng, v, [base + 11], qmax)
     kd, kf = src_dev(torch, k, src, cuda)
     vd, vf = src_dev(torch, v, src, cuda)
     kp, vp, ksc, vsc = garbage_pools(rng, oracle, nb, Hkv, d, quant)
