@@ -128,6 +128,20 @@ __device__ __forceinline__ V stream_load(const V *p) {
 #endif
 }
 
+// Tile loads through a buffer resource covering one tile: a masked tile gets
+// num_records 0, and its loads return zeros without touching memory.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void *tile, int bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void *>(tile), 0, bytes, 0x00020000);
+}
+template <typename T>
+__device__ __forceinline__ T buf_load(__amdgpu_buffer_rsrc_t r, int byte_off) {
+    constexpr int aux = DLMK_MFMA_NT ? 2 : 0;  // nt
+    if constexpr (sizeof(T) == 16)
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b128(r, byte_off, 0, aux));
+    else
+        return __builtin_bit_cast(T, __builtin_amdgcn_raw_buffer_load_b64(r, byte_off, 0, aux));
+}
+
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -349,6 +363,7 @@ struct CodecFloat {  // f16 / bf16 pools: K [d/8][16][8], V [d][16] elements
     using KRaw = typename Op::x8;
     using VRaw = typename Op::x4;
     static constexpr bool kScaled = false;
+    static constexpr bool kBufLoads = true;
     static constexpr int kMinWaves = 1;  // memory-bound at the compiler's allocation
     static constexpr float kBias = 0.f, kBiasK = 0.f;
     static constexpr int64_t kTileBytes = (int64_t)D * kBlock * sizeof(E);
@@ -359,6 +374,11 @@ struct CodecFloat {  // f16 / bf16 pools: K [d/8][16][8], V [d][16] elements
     static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int k, int lane) {
         const int g = lane >> 4, n = lane & 15;
         return stream_load(reinterpret_cast<const VRaw *>(tile) + ((16 * k + n) * kBlock + 4 * g) / 4);
+    }
+    static __device__ __forceinline__ int k_off(int i, int lane) { return (64 * i + lane) * (int)sizeof(KRaw); }
+    static __device__ __forceinline__ int v_off(int k, int lane) {
+        const int g = lane >> 4, n = lane & 15;
+        return ((16 * k + n) * kBlock + 4 * g) / 4 * (int)sizeof(VRaw);
     }
     static __device__ __forceinline__ int q_chunk(int i, int g) { return 4 * i + g; }
     static __device__ __forceinline__ KRaw q_op(KRaw q) { return q; }
@@ -387,6 +407,7 @@ struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
     using KRaw = u32x4;
     using VRaw = u32x4;
     static constexpr bool kScaled = true;
+    static constexpr bool kBufLoads = true;
     static constexpr float kBias = 1024.f + 128.f, kBiasK = kBias;  // bytes c + 128
     static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;
     static constexpr int64_t kTileBytes = (int64_t)D * kBlock;
@@ -397,6 +418,8 @@ struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
     static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int l, int lane) {
         return stream_load(reinterpret_cast<const VRaw *>(tile) + 64 * l + lane);
     }
+    static __device__ __forceinline__ int k_off(int p, int lane) { return (64 * p + lane) * (int)sizeof(KRaw); }
+    static __device__ __forceinline__ int v_off(int l, int lane) { return (64 * l + lane) * (int)sizeof(VRaw); }
     static __device__ __forceinline__ int q_chunk(int i, int g) { return 8 * (i >> 1) + 2 * g + (i & 1); }
     static __device__ __forceinline__ f16x8 q_op(f16x8 q) { return q; }
     static __device__ __forceinline__ f16x8 k_op(KRaw r, int s) {
@@ -417,6 +440,7 @@ struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 
     using KRaw = typename std::conditional<kWide, u32x4, u32x2>::type;
     using VRaw = KRaw;
     static constexpr bool kScaled = true;
+    static constexpr bool kBufLoads = false;  // measured 1 point slower with them
     // K codes are unbiased per element: with codes of at most 7 against a
     // bias of 1032 the f32 cancellation in the scores, scaled by a large
     // token's K scale, reaches the output tolerance.  V keeps the bias (its
@@ -431,6 +455,8 @@ struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 
     static __device__ __forceinline__ VRaw load_v(const uint8_t *tile, int l, int lane) {
         return stream_load(reinterpret_cast<const VRaw *>(tile) + 64 * l + lane);
     }
+    static __device__ __forceinline__ int k_off(int p, int lane) { return (64 * p + lane) * (int)sizeof(KRaw); }
+    static __device__ __forceinline__ int v_off(int l, int lane) { return (64 * l + lane) * (int)sizeof(VRaw); }
     static __device__ __forceinline__ int q_chunk(int i, int g) { return SK * (4 * (i / SK) + g) + i % SK; }
     // k_op emits a word's elements in the order 0 2 4 6 1 3 5 7 (even nibbles, then odd).
     static __device__ __forceinline__ f16x8 q_op(f16x8 q) {
@@ -544,9 +570,14 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     const int limit = n < ROWS ? ctx - NQ + n / GQA + 1 : ctx;
 
     // This wave's blocks: partition block b*NW + wave.  Blocks past the
-    // context (or with an id outside the pool) are masked.  Quantized pools
-    // still load them, pointed at the wave's first block, so that every load
-    // is issued unconditionally; f16 / bf16 pools skip their loads (issue()).
+    // context (or with an id outside the pool) are masked: their loads are
+    // pointed at the wave's first block, so that every load is issued
+    // unconditionally, and with buffer loads (f16 / bf16 and int8 pools) the
+    // tile's resource has no records, so they return zeros without touching
+    // memory.  Re-reads of the first block had partly come from HBM:
+    // configs[1] 71.0 -> 72.9% of HBM peak and traffic 1.047 -> 1.017x the
+    // algorithmic bytes, configs[4] 65.9 -> 67.5%, int8 60.5 -> 61.6%; int4
+    // measured a point slower and keeps global loads of the first block.
     int lbs[NB];
     int64_t blk[NB];
     bool ok[NB];
@@ -637,41 +668,34 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         // scheduling barrier: loads complete in issue order, so waiting for
         // a scale never waits for a later stage's codes.
         auto issue = [&](int t) {
-            // f16 / bf16 pools: masked blocks (past the context, or ids
-            // outside the pool) load nothing -- their scores are -inf and
-            // their V is zeroed below, so the registers are only cleared
-            // (wave-uniform branch).  Configs[1] 70.7 / 71.2 -> 72.3 / 72.5%
-            // of HBM peak, HBM bytes 1.047 -> 1.017x algorithmic; configs[3]
-            // -0.5 points.  The quantized pools measured 12 points slower
-            // with it and load every block (pointed at the wave's first).
-            if constexpr (!C::kScaled) {
-                if (t < 2 * NB && !ok[t < NB ? t : t - NB]) {
-                    if (t < NB) {
-#pragma unroll
-                        for (int i = 0; i < C::KL; ++i) kb[t][i] = typename C::KRaw{};
-                    } else {
-#pragma unroll
-                        for (int l = 0; l < C::VL; ++l) vb[t - NB][l] = typename C::VRaw{};
-                    }
-                    return;
-                }
-            }
             if (t < NB) {
                 if constexpr (C::kScaled) {
                     ksc[t] = *reinterpret_cast<const f32x4 *>(k_scales + blk[t] * kBlock + 4 * g);
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 const uint8_t *kt = k_pool + (blk[t] * num_kv_heads + kvh) * TILE;
+                if constexpr (C::kBufLoads) {
+                    const auto rk = tile_rsrc(kt, ok[t] ? (int)TILE : 0);
 #pragma unroll
-                for (int i = 0; i < C::KL; ++i) kb[t][i] = C::load_k(kt, i, lane);
+                    for (int i = 0; i < C::KL; ++i) kb[t][i] = buf_load<typename C::KRaw>(rk, C::k_off(i, lane));
+                } else {
+#pragma unroll
+                    for (int i = 0; i < C::KL; ++i) kb[t][i] = C::load_k(kt, i, lane);
+                }
             } else if (t < 2 * NB) {
                 if constexpr (C::kScaled) {
                     vsc[t - NB] = *reinterpret_cast<const f32x4 *>(v_scales + blk[t - NB] * kBlock + 4 * g);
                     __builtin_amdgcn_sched_barrier(0);
                 }
                 const uint8_t *vt = v_pool + (blk[t - NB] * num_kv_heads + kvh) * TILE;
+                if constexpr (C::kBufLoads) {
+                    const auto rv = tile_rsrc(vt, ok[t - NB] ? (int)TILE : 0);
 #pragma unroll
-                for (int l = 0; l < C::VL; ++l) vb[t - NB][l] = C::load_v(vt, l, lane);
+                    for (int l = 0; l < C::VL; ++l) vb[t - NB][l] = buf_load<typename C::VRaw>(rv, C::v_off(l, lane));
+                } else {
+#pragma unroll
+                    for (int l = 0; l < C::VL; ++l) vb[t - NB][l] = C::load_v(vt, l, lane);
+                }
             }
         };
 #pragma unroll
