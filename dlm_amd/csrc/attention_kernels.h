@@ -440,7 +440,7 @@ struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 
     using KRaw = typename std::conditional<kWide, u32x4, u32x2>::type;
     using VRaw = KRaw;
     static constexpr bool kScaled = true;
-    static constexpr bool kBufLoads = false;  // measured 1 point slower with them
+    static constexpr bool kBufLoads = false;  // measured slower with them (configs[3] -1.3 points)
     // K codes are unbiased per element: with codes of at most 7 against a
     // bias of 1032 the f32 cancellation in the scores, scaled by a large
     // token's K scale, reaches the output tolerance.  V keeps the bias (its
