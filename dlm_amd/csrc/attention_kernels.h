@@ -337,6 +337,19 @@ __device__ __forceinline__ f16x4 biased4(uint32_t w) {
     return f16x4{a[0], a[1], b[0], b[1]};
 }
 
+// Four bytes of w whose low nibbles are zero -> f16x4 of 1 + byte / 1024: the
+// byte goes under a 0x3C high byte (exponent 0), so a nibble n held in the
+// byte's high half becomes 1 + n / 64.  With the nibble in mantissa bits 4-7
+// instead of 0-3, the bias is 72 code units (1 + 8/64 against a unit of 1/64)
+// rather than 1032: small enough for the kernel to remove it from the score
+// after the dot product, as for int8 codes (1152 units against codes 16x
+// larger).
+__device__ __forceinline__ f16x4 unit4(uint32_t w) {
+    const f16x2 a = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x3c3c3c3cu, w, 0x04010400u));
+    const f16x2 b = __builtin_bit_cast(f16x2, __builtin_amdgcn_perm(0x3c3c3c3cu, w, 0x04030402u));
+    return f16x4{a[0], a[1], b[0], b[1]};
+}
+
 // Storage codecs of the matrix-core kernel, one per pool format and head
 // dim D.  A codec says where a lane's K and V bytes sit in a (block, kv head)
 // tile and how they become MFMA operands:
@@ -365,7 +378,7 @@ struct CodecFloat {  // f16 / bf16 pools: K [d/8][16][8], V [d][16] elements
     static constexpr bool kScaled = false;
     static constexpr bool kBufLoads = true;
     static constexpr int kMinWaves = 1;  // memory-bound at the compiler's allocation
-    static constexpr float kBias = 0.f, kBiasK = 0.f;
+    static constexpr float kBias = 0.f, kBiasK = 0.f, kKScale = 1.f;
     static constexpr int64_t kTileBytes = (int64_t)D * kBlock * sizeof(E);
     static constexpr int SK = 1, KL = D / 32, SV = 1, VL = D / 16;
     static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int i, int lane) {
@@ -408,7 +421,7 @@ struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
     using VRaw = u32x4;
     static constexpr bool kScaled = true;
     static constexpr bool kBufLoads = true;
-    static constexpr float kBias = 1024.f + 128.f, kBiasK = kBias;  // bytes c + 128
+    static constexpr float kBias = 1024.f + 128.f, kBiasK = kBias, kKScale = 1.f;  // bytes c + 128
     static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;
     static constexpr int64_t kTileBytes = (int64_t)D * kBlock;
     static constexpr int SK = 2, KL = D / 64, SV = 4, VL = D / 64;
@@ -441,11 +454,15 @@ struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 
     using VRaw = KRaw;
     static constexpr bool kScaled = true;
     static constexpr bool kBufLoads = false;  // measured slower with them (configs[3] -1.3 points)
-    // K codes are unbiased per element: with codes of at most 7 against a
-    // bias of 1032 the f32 cancellation in the scores, scaled by a large
-    // token's K scale, reaches the output tolerance.  V keeps the bias (its
-    // error is relative to p * v_scale, which the output is divided by).
-    static constexpr float kBias = 1024.f + 8.f, kBiasK = 0.f;  // nibbles c + 8
+    // K nibbles widen to 1 + (c + 8) / 64 (unit4): the score is
+    // (dot - 1.125 * sum(q)) * k_scale * 64, the 64 folded into the softmax
+    // scale.  The 0x64 widening of the V codes
+    // (B + c, B = 1032) would put a 1032-unit bias on K as well, whose f32
+    // cancellation in the scores, scaled by a large token's K scale, reached
+    // the output tolerance; the V bias is relative to p * v_scale, which the
+    // output is divided by.
+    static constexpr float kBias = 1024.f + 8.f;  // V nibbles c + 8
+    static constexpr float kBiasK = 1.125f, kKScale = 64.f;
     static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;
     static constexpr int64_t kTileBytes = (int64_t)D * kBlock / 2;
     static constexpr int SK = KG / 8, KL = D / (4 * KG), SV = VG, VL = D / (16 * VG);
@@ -464,9 +481,8 @@ struct CodecI4 {  // KG, VG = 32, 8 (D % 128 == 0: 16-byte loads) or 16, 4 (D = 
     }
     static __device__ __forceinline__ f16x8 k_op(KRaw r, int s) {
         const uint32_t x = r[s];  // nibbles c + 8
-        const f16x4 a = biased4(x & 0x0f0f0f0fu), b = biased4((x >> 4) & 0x0f0f0f0fu);
-        const f16x8 w = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
-        return w - (_Float16)kBias;
+        const f16x4 a = unit4((x << 4) & 0xf0f0f0f0u), b = unit4(x & 0xf0f0f0f0u);
+        return f16x8{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
     }
     // Word kk / 2 holds dims kk & ~1 (low nibbles) and kk | 1 of 4 tokens.
     static __device__ __forceinline__ f16x4 v_op(VRaw r, int kk) {
@@ -708,6 +724,8 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         // Sum of row n's Q operand (as the MFMA sees it): the score bias is
         // kBiasK * qsum.
         float qsum = 0.f;
+        // Softmax scale with the codec's score unit folded in (exact: a power of two).
+        const float sl2 = scale_log2 * C::kKScale;
         if constexpr (C::kBiasK != 0.f) {
 #pragma unroll
             for (int i = 0; i < KI; ++i)
@@ -749,12 +767,12 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
                 ok[b] && (lbs[b] + 1) * kBlock <= ctx - NQ + 1);
             if (full) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) s[b][j] = c[j] * scale_log2;
+                for (int j = 0; j < 4; ++j) s[b][j] = c[j] * sl2;
             } else {
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     const int pos = lbs[b] * kBlock + 4 * g + j;
-                    s[b][j] = (ok[b] && pos < limit) ? c[j] * scale_log2 : -INFINITY;
+                    s[b][j] = (ok[b] && pos < limit) ? c[j] * sl2 : -INFINITY;
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -767,6 +785,9 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
             for (int j = 0; j < 4; ++j) m = fmaxf(m, s[b][j]);
         m = fmaxf(m, __shfl_xor(m, 16));
         m = fmaxf(m, __shfl_xor(m, 32));
+        // A row with no valid score (m = -inf) subtracts 0 instead: its
+        // scores are all -inf and exponentiate to 0 without a select per score.
+        const float msub = m == -INFINITY ? 0.f : m;
 
         // O += P . V.  Float pools: P rounded to the operand type, and l sums
         // the rounded P.  Quantized pools: the operand is p * v_scale (l sums
@@ -779,14 +800,27 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
             // maybe NaN) or belong to a masked block (another block's bytes).
             const int valid = __builtin_amdgcn_readfirstlane(ok[b] ? ctx - lbs[b] * kBlock : 0);
             x4 pa;
+            // v_exp_f32 directly: s - m <= 0 (or -inf, giving 0), and
+            // results below 2^-126 (flushed) do not matter next to the row max's 1.
+            float p4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p4[j] = __builtin_amdgcn_exp2f(s[b][j] - msub);
+            if constexpr (C::kScaled) {
+                // Past `valid` p is 0 already; the select keeps a NaN scale
+                // out.  int4: blocks wholly inside the context skip it
+                // (wave-uniform; the int8 kernel spills with the branch).
+                if (C::kCodeBits == 4 && valid >= kBlock) {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) pa[j] = (PT)(p4[j] * vsc[b][j]);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) pa[j] = (PT)(4 * g + j < valid ? p4[j] * vsc[b][j] : 0.f);
+                }
+            }
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
-                // v_exp_f32 directly: s - m <= 0 (or -inf, giving 0), and
-                // results below 2^-126 (flushed) do not matter next to the row max's 1.
-                const float p = m == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(s[b][j] - m);
+                const float p = p4[j];
                 if constexpr (C::kScaled) {
-                    // p is 0 there already; the select keeps a NaN scale out.
-                    pa[j] = (PT)(valid >= kBlock || 4 * g + j < valid ? p * vsc[b][j] : 0.f);
                     lsum += p;
                 } else {
                     const PT ph = (PT)p;
