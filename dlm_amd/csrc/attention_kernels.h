@@ -105,6 +105,18 @@ constexpr float kLog2e = 1.4426950408889634f;
 #ifndef DLMK_MFMA_WPE
 #define DLMK_MFMA_WPE 0
 #endif
+// Quantized pools that run paged_attn_packed_kernel (bit 0: int4 with at
+// most 8 query rows, bit 1: int8 with at most 4, bit 2: int8 with 5-8).
+// Measured at configs[1] (4 rows) and configs[3] (8 rows), attention only:
+// int4 47.4 -> 49.6% and 55.0 -> 57.3% of HBM peak; int8 63.9 -> 65.5% with
+// 4 rows but 67.9 -> 64.2% with 8.
+#ifndef DLMK_MFMA_PACKED
+#define DLMK_MFMA_PACKED 3
+#endif
+// Blocks per wave for int8 pools.
+#ifndef DLMK_MFMA_Q8NB
+#define DLMK_MFMA_Q8NB 16
+#endif
 // 1: stream K/V tiles with non-temporal loads (no reuse, keep them out of L2/MALL).
 #ifndef DLMK_MFMA_NT
 #define DLMK_MFMA_NT 1
@@ -424,6 +436,7 @@ struct CodecI8 {  // KG = 16, VG = 4: 16-byte K and V loads
     static constexpr float kBias = 1024.f + 128.f, kBiasK = kBias, kKScale = 1.f;  // bytes c + 128
     static constexpr int kMinWaves = D <= 128 ? DLMK_MFMA_QWAVES : 1;
     static constexpr int64_t kTileBytes = (int64_t)D * kBlock;
+    static constexpr int KG = 16, VG = 4;  // dims per K / V load of a lane
     static constexpr int SK = 2, KL = D / 64, SV = 4, VL = D / 64;
     static __device__ __forceinline__ KRaw load_k(const uint8_t *tile, int p, int lane) {
         return stream_load(reinterpret_cast<const KRaw *>(tile) + 64 * p + lane);
@@ -888,6 +901,342 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     if (g == 0 && n < ROWS) {
         ml_lds[wave][n][0] = m;
         ml_lds[wave][n][1] = lsum;
+    }
+    __syncthreads();
+    merge_waves<ROWS, D, NW, GQA, NQ>(o_lds, ml_lds, out, out_dtype, seq, kvh, part, nparts,
+                                      num_q_heads, max_parts, ws_o, ws_ml);
+}
+
+
+// ---------------------------------------------------------------------------
+// Packed matrix-core kernel for quantized pools and query groups of at most 8
+// rows (GQA group x verify queries).  paged_attn_mfma_kernel gives every
+// 16-token block its own 16-column score tile, so with 4 rows 12 of the 16
+// columns are padding: their scores, softmax arithmetic and registers are
+// spent for nothing.  Here one MFMA tile holds T = 16 / RP blocks (RP = 4 or
+// 8 columns a block), block tau of a group of T in columns RP*tau .. +RP-1:
+//
+//   S^T (16 tokens x (T blocks x RP rows)) = sum over 16-lane groups g of
+//       K_{block of g} (16 x 8 dims) . Qdiag (8 dims x 16 columns)
+//   Lane group g always feeds the same block tau(g) = g / (4 / T) of the
+//   group (all of its token's K row for T = 4, half of it for T = 2); the B
+//   operand is Q in the columns of block tau(g) and zero elsewhere (block
+//   diagonal).  It is read from LDS: each lane's address is fixed for the
+//   launch (its row of Q, or a zero line when its column belongs to another
+//   block), so the operand costs one ds_read and no VALU per step.
+//   The accumulator leaves lane (column n, group g) with tokens 4g..4g+3 of
+//   block n / RP, row n % RP: every lane holds real scores.
+//
+//   O^T (16 dims x (T x RP)) += V^T (16 dims x 16 tokens) . Pdiag (16 tokens x 16)
+//   At step sigma lane group g feeds token quad g ^ (sigma * 4 / T) of its
+//   block's V; the matching P values sit in lane group g ^ (sigma * 4 / T) of
+//   the same column, fetched by one xor shuffle and zeroed where the column
+//   belongs to another block.  The T blocks' partial outputs of a row are
+//   summed across columns (DPP row rotations) once per wave.
+//
+// Same MFMA count per block as the unpacked kernel, 4x (T = 4) fewer scores
+// per lane, and no zero query rows in the score arithmetic.
+// ---------------------------------------------------------------------------
+// arr[base + idx] for a lane-varying idx < T over wave-uniform arr: a select
+// chain on values made explicitly scalar (readfirstlane), so the compiler
+// cannot turn it back into an indexed load from a stack copy of arr.
+__device__ __forceinline__ int64_t uniform(int64_t v) {
+    const uint64_t u = (uint64_t)v;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+    return (int64_t)(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ bool uniform(bool v) { return __builtin_amdgcn_readfirstlane((int)v) != 0; }
+
+
+// v + v rotated by R lanes within each row of 16 (DPP row_ror).
+template <int R>
+__device__ __forceinline__ float row_ror_add(float v) {
+    const int r = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x120 + R, 0xf, 0xf, false);
+    return v + __builtin_bit_cast(float, r);
+}
+
+template <typename C, int D, int GQA, int NQ, int NW, int NB, int PD>
+__global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_packed_kernel(
+    void *__restrict__ out, int out_dtype, const typename C::QT *__restrict__ q,
+    const uint8_t *__restrict__ k_pool, const uint8_t *__restrict__ v_pool,
+    const float *__restrict__ k_scales, const float *__restrict__ v_scales,
+    const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
+    int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
+    int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
+    using M = typename C::Op;
+    using x8 = typename M::x8;
+    using x4 = typename M::x4;
+    using PT = typename M::elem;
+    using QT = typename C::QT;
+    using KRaw = typename C::KRaw;
+    using VRaw = typename C::VRaw;
+    constexpr int ROWS = GQA * NQ;
+    static_assert(C::kScaled && ROWS <= 8 && D % 64 == 0, "packed kernel: quantized pools, <= 8 rows");
+    constexpr int RP = ROWS <= 4 ? 4 : 8;  // columns per block
+    constexpr int T = 16 / RP;             // blocks per MFMA tile
+    constexpr int G = 4 / T;               // lane groups per block
+    constexpr int NG = NB / T;             // block groups per wave
+    static_assert(NB % T == 0, "blocks per wave must fill the block groups");
+    constexpr int CH = D / 8 / G;          // 8-dim chunks a lane group feeds per block = QK steps per group
+    constexpr int SK = C::KG / 8;          // chunks per K load
+    constexpr int NLK = CH / SK;           // K loads per lane per group
+    constexpr int NLV = T * C::VL;         // V loads per lane per group
+    constexpr int NK = NG * NLK, NV = NG * NLV;
+    constexpr int QS = CH;                 // QK steps per group
+    constexpr int QP = 3;                  // Q operand reads in flight ahead of the MFMAs
+    constexpr int VN = D / 16;
+    constexpr int P = NW * NB * kBlock;
+    constexpr int64_t TILE = C::kTileBytes;
+
+    __shared__ float o_lds[NW][ROWS][D];
+    __shared__ float ml_lds[NW][ROWS][2];
+    // Q rows in operand order, then one zero line.
+    __shared__ __attribute__((aligned(16))) QT q_lds[RP * D + CH * 8];
+    __shared__ float qsum_lds[RP];
+
+    const int part = gridDim.y - 1 - blockIdx.y;
+    const int kvh = blockIdx.x % num_kv_heads, seq = blockIdx.x / num_kv_heads;
+    const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
+    const int nparts = parts_of(ctx, P);
+    if (part >= nparts) return;
+
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, n = lane & 15;
+    const int tcol = n / RP, r = n % RP;   // this lane's score column: block tcol of a group, row r
+    const int tg = g / G, gs = g % G;      // block this lane group feeds, and its part of the K row
+    const int nblk_seq = (ctx + kBlock - 1) / kBlock;
+    const int32_t *table = block_tables + (int64_t)seq * max_blocks;
+
+    // Stage Q (operand order, rows past ROWS zero) and each row's operand sum.
+    {
+        constexpr int CPR = D / 8;  // chunks per row
+        static_assert(RP * CPR <= NW * 64, "one chunk per thread");
+        const int idx = threadIdx.x;
+        if (idx < RP * CPR) {
+            const int rr = idx / CPR, c = idx % CPR;
+            x8 v = {};
+            if (rr < ROWS) {
+                const int j = rr / GQA, h = kvh * GQA + rr % GQA;
+                v = C::q_op(reinterpret_cast<const x8 *>(q + ((int64_t)(seq * NQ + j) * num_q_heads + h) * D)[c]);
+            }
+            *reinterpret_cast<x8 *>(&q_lds[rr * D + 8 * c]) = v;
+            float sum = 0.f;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) sum += (float)v[e];
+#pragma unroll
+            for (int o = 1; o < CPR; o <<= 1) sum += __shfl_xor(sum, o);
+            if (c == 0) qsum_lds[rr] = sum;
+        }
+        for (int e = threadIdx.x; e < CH; e += NW * 64) *reinterpret_cast<x8 *>(&q_lds[RP * D + 8 * e]) = x8{};
+    }
+
+    // Logical block of this wave's b-th block and its validity (wave-uniform
+    // bit mask).  Each lane also reads, per block group, the pool ids of the
+    // block its lane group loads (tg) and of its score column's block (tcol):
+    // a clamped table index, and block 0 for ids outside the pool, so every
+    // load is issued unconditionally and stays inside the pool.
+    const auto lbof = [&](int b) { return part * (NW * NB) + wave_block(b, NB) * NW + wave; };
+    uint32_t okm = 0;
+    {
+        int32_t bid[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b) bid[b] = table[max(min(lbof(b), nblk_seq - 1), 0)];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+            okm |= (uint32_t)(lbof(b) < nblk_seq && bid[b] >= 0 && bid[b] < num_blocks) << b;
+    }
+    const int nvalid = __builtin_popcount(okm);
+    int32_t idt[NG], ids[NG];
+#pragma unroll
+    for (int u = 0; u < NG; ++u) {
+        idt[u] = table[max(min(lbof(u * T + tg), nblk_seq - 1), 0)];
+        ids[u] = table[max(min(lbof(u * T + tcol), nblk_seq - 1), 0)];
+    }
+    __syncthreads();
+
+    float m = -INFINITY, lsum = 0.f;
+    f32x4 accp = {0.f, 0.f, 0.f, 0.f};
+    f32x4 acc[VN];
+#pragma unroll
+    for (int k = 0; k < VN; ++k) acc[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const int limit = r < ROWS ? ctx - NQ + r / GQA + 1 : ctx;
+
+    if (nvalid > 0) {
+        // This lane's Q operand line: its row's chunks for its part of the K
+        // row, or zeros when its column belongs to another block.
+        const int qline = (tcol == tg && r < ROWS) ? r * D + gs * CH * 8 : RP * D;
+        const float qsum = qsum_lds[r];
+        const float sl2 = scale_log2 * C::kKScale;
+
+        const auto inpool = [&](int32_t id) { return id >= 0 && id < num_blocks ? id : 0; };
+        KRaw kr[NK];
+        VRaw vr[NV];
+        f32x4 ksc[NG], vsc[NG];
+        int64_t kto[NG], vto[NG];  // this lane group's tile offset in group u
+        // Flat load sequence: the groups' K loads, then their V loads; the
+        // scales of a group go out before its first code load.
+        auto issue = [&](int t) {
+            if (t < NK) {
+                const int u = t / NLK, x = t % NLK;
+                if (x == 0) {
+                    ksc[u] = *reinterpret_cast<const f32x4 *>(k_scales + (int64_t)inpool(ids[u]) * kBlock + 4 * g);
+                    __builtin_amdgcn_sched_barrier(0);
+                    kto[u] = ((int64_t)inpool(idt[u]) * num_kv_heads + kvh) * TILE;
+                }
+                const KRaw *kt = reinterpret_cast<const KRaw *>(k_pool + kto[u]);
+                kr[t] = stream_load(kt + (gs * NLK + x) * kBlock + n);
+            } else if (t < NK + NV) {
+                const int tv = t - NK;
+                const int u = tv / NLV, y = tv % NLV, sg = y / C::VL, l = y % C::VL;
+                if (y == 0) {
+                    vsc[u] = *reinterpret_cast<const f32x4 *>(v_scales + (int64_t)inpool(ids[u]) * kBlock + 4 * g);
+                    __builtin_amdgcn_sched_barrier(0);
+                    vto[u] = ((int64_t)inpool(idt[u]) * num_kv_heads + kvh) * TILE;
+                }
+                const VRaw *vt = reinterpret_cast<const VRaw *>(v_pool + vto[u]);
+                vr[tv] = stream_load(vt + 64 * l + 16 * (g ^ (sg * G)) + n);
+            }
+        };
+#pragma unroll
+        for (int t = 0; t < PD; ++t) issue(t);
+        __builtin_amdgcn_sched_barrier(0);
+
+        // Scores: s[u][j] = row r, token 4g + j of block u*T + tcol.
+        float s[NG][4];
+#pragma unroll
+        for (int u = 0; u < NG; ++u) {
+            f32x4 c = {0.f, 0.f, 0.f, 0.f}, c1 = {0.f, 0.f, 0.f, 0.f};
+            // The Q operand is re-read from LDS for every group: an opaque
+            // copy of the line offset keeps the compiler from holding all
+            // QS operands in registers across groups.
+            int ql = qline;
+            asm volatile("" : "+v"(ql));
+            // Operand reads run QP steps ahead of their MFMA (LDS latency).
+            x8 bq[QS];
+#pragma unroll
+            for (int i = 0; i < QP && i < QS; ++i) bq[i] = *reinterpret_cast<const x8 *>(&q_lds[ql + 8 * i]);
+#pragma unroll
+            for (int x = 0; x < NLK; ++x) {
+                issue(u * NLK + x + PD);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int e = 0; e < SK; ++e) {
+                    const int i = x * SK + e;
+                    if (i + QP < QS) bq[i + QP] = *reinterpret_cast<const x8 *>(&q_lds[ql + 8 * (i + QP)]);
+                    if (i & 1)
+                        c1 = M::qk(C::k_op(kr[u * NLK + x], e), bq[i], c1);
+                    else
+                        c = M::qk(C::k_op(kr[u * NLK + x], e), bq[i], c);
+                }
+            }
+            c += c1;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) c[j] = fmaf(-C::kBiasK, qsum, c[j]) * ksc[u][j];
+            bool full = true;
+#pragma unroll
+            for (int tau = 0; tau < T; ++tau)
+                full = full && ((okm >> (u * T + tau)) & 1) && (lbof(u * T + tau) + 1) * kBlock <= ctx - NQ + 1;
+            if (full) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) s[u][j] = c[j] * sl2;
+            } else {
+                const int lb = part * (NW * NB) + wave_block(u * T + tcol, NB) * NW + wave;
+                const bool okc = (okm >> (u * T + tcol)) & 1;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int pos = lb * kBlock + 4 * g + j;
+                    s[u][j] = (okc && pos < limit) ? c[j] * sl2 : -INFINITY;
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+
+        // Row max over every block group and lane of the row (columns
+        // RP*t + r for all t, all lane groups).
+#pragma unroll
+        for (int u = 0; u < NG; ++u)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) m = fmaxf(m, s[u][j]);
+#pragma unroll
+        for (int o = RP; o < 64; o <<= 1) m = fmaxf(m, __shfl_xor(m, o));
+        const float msub = m == -INFINITY ? 0.f : m;
+
+        const x4 ones = {(PT)1.f, (PT)1.f, (PT)1.f, (PT)1.f};
+#pragma unroll
+        for (int u = 0; u < NG; ++u) {
+            float p4[4];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) p4[j] = __builtin_amdgcn_exp2f(s[u][j] - msub);
+            bool full = true;
+#pragma unroll
+            for (int tau = 0; tau < T; ++tau)
+                full = full && ((okm >> (u * T + tau)) & 1) && (lbof(u * T + tau) + 1) * kBlock <= ctx;
+            x4 pa;
+            if (full) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) pa[j] = (PT)(p4[j] * vsc[u][j]);
+            } else {
+                // Past `valid` p is 0 already; the select keeps a NaN scale out.
+                const int lb = part * (NW * NB) + wave_block(u * T + tcol, NB) * NW + wave;
+                const int valid = ((okm >> (u * T + tcol)) & 1) ? ctx - lb * kBlock : 0;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) pa[j] = (PT)(4 * g + j < valid ? p4[j] * vsc[u][j] : 0.f);
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) lsum += p4[j];
+            const u32x2 pw = __builtin_bit_cast(u32x2, pa);
+#pragma unroll
+            for (int sg = 0; sg < T; ++sg) {
+#pragma unroll
+                for (int l = 0; l < C::VL; ++l) {
+                    issue(NK + u * NLV + sg * C::VL + l + PD);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                // P of this step: token quad g ^ (sg * G) of column block tcol,
+                // held by lane group g ^ (sg * G); zero outside block tg's columns.
+                u32x2 w = pw;
+                if (sg != 0) {
+                    w[0] = __shfl_xor(pw[0], 16 * sg * G);
+                    w[1] = __shfl_xor(pw[1], 16 * sg * G);
+                }
+                const x4 bp = tcol == tg ? __builtin_bit_cast(x4, w) : x4{};
+                accp = M::pv(ones, bp, accp);
+#pragma unroll
+                for (int k = 0; k < VN; ++k) {
+                    const x4 vo = C::v_op(vr[u * NLV + sg * C::VL + k / C::SV], k % C::SV);
+                    acc[k] = M::pv(vo, bp, acc[k]);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+            }
+        }
+    }
+#pragma unroll
+    for (int o = RP; o < 64; o <<= 1) lsum += __shfl_xor(lsum, o);
+    // Output bias of column n: kBias * (its P operand sum); then the T blocks'
+    // partials of row r (columns r, RP + r, ...) are summed.
+#pragma unroll
+    for (int k = 0; k < VN; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float v = acc[k][j] - C::kBias * accp[j];
+            if constexpr (T == 4) v = row_ror_add<8>(row_ror_add<4>(v));
+            else v = row_ror_add<8>(v);
+            acc[k][j] = v;
+        }
+
+    // acc[k][j] (columns n < RP) = O[row n][dim v_dim(k, 4g + j)].
+    if (n < ROWS) {
+#pragma unroll
+        for (int k = 0; k < VN; ++k)
+#pragma unroll
+            for (int j = 0; j < 4; ++j) o_lds[wave][n][C::v_dim(k, 4 * g + j)] = acc[k][j];
+        if (g == 0) {
+            ml_lds[wave][n][0] = m;
+            ml_lds[wave][n][1] = lsum;
+        }
     }
     __syncthreads();
     merge_waves<ROWS, D, NW, GQA, NQ>(o_lds, ml_lds, out, out_dtype, seq, kvh, part, nparts,
@@ -1478,6 +1827,15 @@ int launch_mfma_nb(const Args &a) {
     using QT = typename C::QT;
     return launch_pair(a, NW * NB * kBlock, (int64_t)a.B * a.Hkv,
                        [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
+        constexpr int kPackBit = C::kCodeBits == 4 ? 1 : GQA * NQ <= 4 ? 2 : 4;
+        if constexpr (C::kScaled && GQA * NQ <= 8 && (DLMK_MFMA_PACKED & kPackBit)) {
+            hipLaunchKernelGGL((paged_attn_packed_kernel<C, D, GQA, NQ, NW, NB, PD>), grid, dim3(NW * 64), 0,
+                               a.stream, a.out, a.out_dtype, static_cast<const QT *>(a.q),
+                               static_cast<const uint8_t *>(a.k_pool), static_cast<const uint8_t *>(a.v_pool),
+                               a.k_scales, a.v_scales, a.tables, a.ctx_lens, a.Hq, a.Hkv, a.max_blocks,
+                               a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
+            return;
+        }
         // Fused decode step: one more grid row of append work-groups.
         if (!C::kScaled && a.k_new != nullptr) grid.y += 1;
         hipLaunchKernelGGL((paged_attn_mfma_kernel<C, D, GQA, NQ, NW, NB, PD>), grid, dim3(NW * 64), 0,
@@ -1507,6 +1865,7 @@ int launch_mfma(const Args &a) {
         if (parts_for(a.max_blocks, DLMK_MFMA_NW * NBS * kBlock) <= kCombineBatch)
             return launch_mfma_nb<C, D, GQA, NQ, NBS>(a);
     }
+    if constexpr (C::kScaled && C::kCodeBits == 8) return launch_mfma_nb<C, D, GQA, NQ, DLMK_MFMA_Q8NB>(a);
     return launch_mfma_nb<C, D, GQA, NQ, DLMK_MFMA_NB>(a);
 }
 
