@@ -100,6 +100,17 @@ constexpr float kLog2e = 1.4426950408889634f;
 #ifndef DLMK_MFMA_PDQ
 #define DLMK_MFMA_PDQ 2
 #endif
+// Prefetch depth of paged_attn_packed_kernel, in 16-byte loads per lane, for
+// 4 blocks per score tile (groups of up to 4 rows) and for 2 (5-8 rows).
+// Measured (attention only, two runs): 4 blocks, configs[1]: int4 50.4 /
+// 52.2 / 52.0% of HBM peak at depth 2 / 4 / 8, int8 65.3 / 67.0 / 67.5%;
+// 2 blocks, configs[3] int4: 56.9 / 54.0 / 54.4% at depth 2 / 4 / 8.
+#ifndef DLMK_MFMA_PDP4
+#define DLMK_MFMA_PDP4 8
+#endif
+#ifndef DLMK_MFMA_PDP2
+#define DLMK_MFMA_PDP2 2
+#endif
 // Minimum waves per SIMD the register allocation must allow for every pool
 // format (0: per-format defaults above; a tuning override).
 #ifndef DLMK_MFMA_WPE
@@ -1829,7 +1840,8 @@ int launch_mfma_nb(const Args &a) {
                        [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
         constexpr int kPackBit = C::kCodeBits == 4 ? 1 : GQA * NQ <= 4 ? 2 : 4;
         if constexpr (C::kScaled && GQA * NQ <= 8 && (DLMK_MFMA_PACKED & kPackBit)) {
-            hipLaunchKernelGGL((paged_attn_packed_kernel<C, D, GQA, NQ, NW, NB, PD>), grid, dim3(NW * 64), 0,
+            constexpr int PDP = GQA * NQ <= 4 ? DLMK_MFMA_PDP4 : DLMK_MFMA_PDP2;
+            hipLaunchKernelGGL((paged_attn_packed_kernel<C, D, GQA, NQ, NW, NB, PDP>), grid, dim3(NW * 64), 0,
                                a.stream, a.out, a.out_dtype, static_cast<const QT *>(a.q),
                                static_cast<const uint8_t *>(a.k_pool), static_cast<const uint8_t *>(a.v_pool),
                                a.k_scales, a.v_scales, a.tables, a.ctx_lens, a.Hq, a.Hkv, a.max_blocks,
