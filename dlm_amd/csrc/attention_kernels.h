@@ -948,19 +948,6 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
 // Same MFMA count per block as the unpacked kernel, 4x (T = 4) fewer scores
 // per lane, and no zero query rows in the score arithmetic.
 // ---------------------------------------------------------------------------
-// arr[base + idx] for a lane-varying idx < T over wave-uniform arr: a select
-// chain on values made explicitly scalar (readfirstlane), so the compiler
-// cannot turn it back into an indexed load from a stack copy of arr.
-__device__ __forceinline__ int64_t uniform(int64_t v) {
-    const uint64_t u = (uint64_t)v;
-    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
-    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
-    return (int64_t)(((uint64_t)hi << 32) | lo);
-}
-__device__ __forceinline__ int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
-__device__ __forceinline__ bool uniform(bool v) { return __builtin_amdgcn_readfirstlane((int)v) != 0; }
-
-
 // v + v rotated by R lanes within each row of 16 (DPP row_ror).
 template <int R>
 __device__ __forceinline__ float row_ror_add(float v) {
