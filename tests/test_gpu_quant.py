@@ -228,6 +228,11 @@ def quant_workload(oracle, rng, ctx, Hkv, d, quant):
     ([600, 4, 90], 16, 4, 128, 4),           # 4-query verify
     ([777, 16], 32, 2, 256, 1),              # GQA 16, d 256
     ([333], 8, 8, 64, 2),                    # MHA, 2 queries
+    # Groups of up to 8 rows run the packed kernel (several blocks per score tile):
+    ([900, 20, 1500], 32, 8, 128, 2),        # GQA 4 x 2 queries: 8 rows, 2 blocks a tile (int4)
+    ([640, 33], 16, 8, 64, 2),               # GQA 2 x 2 queries: 4 rows, d 64
+    ([1100, 7], 8, 8, 256, 4),               # GQA 1 x 4 queries: 4 rows, d 256
+    ([1030, 300], 64, 8, 64, 1),             # GQA 8 at d 64 (int4: 8-byte code loads)
 ])
 def test_attention_quant_matches_oracle(oracle, torch_mod, ops, cuda, qname, ctx, Hq, Hkv, d, nq):
     torch = torch_mod
