@@ -990,8 +990,11 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_packed_ker
 
     __shared__ float o_lds[NW][ROWS][D];
     __shared__ float ml_lds[NW][ROWS][2];
-    // Q rows in operand order, then one zero line.
-    __shared__ __attribute__((aligned(16))) QT q_lds[RP * D + CH * 8];
+    // Q rows in operand order, then one zero line.  Rows are padded by 16
+    // bytes: at D * 2 bytes apart (a multiple of the 256-byte bank cycle) the
+    // rows one read instruction touches would sit in the same banks.
+    constexpr int QSTR = D + 8;
+    __shared__ __attribute__((aligned(16))) QT q_lds[RP * QSTR + CH * 8];
     __shared__ float qsum_lds[RP];
 
     const int part = gridDim.y - 1 - blockIdx.y;
@@ -1020,7 +1023,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_packed_ker
                 const int j = rr / GQA, h = kvh * GQA + rr % GQA;
                 v = C::q_op(reinterpret_cast<const x8 *>(q + ((int64_t)(seq * NQ + j) * num_q_heads + h) * D)[c]);
             }
-            *reinterpret_cast<x8 *>(&q_lds[rr * D + 8 * c]) = v;
+            *reinterpret_cast<x8 *>(&q_lds[rr * QSTR + 8 * c]) = v;
             float sum = 0.f;
 #pragma unroll
             for (int e = 0; e < 8; ++e) sum += (float)v[e];
@@ -1028,7 +1031,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_packed_ker
             for (int o = 1; o < CPR; o <<= 1) sum += __shfl_xor(sum, o);
             if (c == 0) qsum_lds[rr] = sum;
         }
-        for (int e = threadIdx.x; e < CH; e += NW * 64) *reinterpret_cast<x8 *>(&q_lds[RP * D + 8 * e]) = x8{};
+        for (int e = threadIdx.x; e < CH; e += NW * 64) *reinterpret_cast<x8 *>(&q_lds[RP * QSTR + 8 * e]) = x8{};
     }
 
     // Logical block of this wave's b-th block and its validity (wave-uniform
@@ -1065,7 +1068,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_packed_ker
     if (nvalid > 0) {
         // This lane's Q operand line: its row's chunks for its part of the K
         // row, or zeros when its column belongs to another block.
-        const int qline = (tcol == tg && r < ROWS) ? r * D + gs * CH * 8 : RP * D;
+        const int qline = (tcol == tg && r < ROWS) ? r * QSTR + gs * CH * 8 : RP * QSTR;
         const float qsum = qsum_lds[r];
         const float sl2 = scale_log2 * C::kKScale;
 
