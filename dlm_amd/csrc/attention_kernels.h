@@ -529,7 +529,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     const typename C::QT *__restrict__ k_new, const typename C::QT *__restrict__ v_new,
     const int32_t *__restrict__ block_tables, const int32_t *__restrict__ ctx_lens,
     int num_q_heads, int num_kv_heads, int max_blocks, int64_t num_blocks, float scale_log2,
-    int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml) {
+    int max_parts, float *__restrict__ ws_o, float *__restrict__ ws_ml, int append_row) {
     using M = typename C::Op;
     using x8 = typename M::x8;
     using x4 = typename M::x4;
@@ -555,10 +555,13 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     // the short sequences' small work-groups fill the drain (+1 point of HBM
     // peak over first-index-first at the 8B shape).
     if constexpr (!C::kScaled) {
-        // Fused decode step: the first row of the grid (dealt first) stores
-        // the new tokens, one work-group per sequence (the row's work-groups
-        // of kv head 0) covering all its kv heads; the partition work-groups
-        // take them from k_new / v_new in registers instead of the pools.
+        // Fused decode step: the partition work-groups take the new tokens
+        // from k_new / v_new in registers instead of the pools.  When a
+        // combine launch follows, it stores them into the pools (configs[1]
+        // step 100.4 -> 99.9 us against 97.7 for the attention pair);
+        // otherwise the first row of the grid (dealt first) does, one
+        // work-group per sequence (the row's work-groups of kv head 0)
+        // covering all its kv heads.
         // Measured at the 8B shape (configs[1], step / attention alone):
         //   stores issued by the partition waves themselves, behind a fence:
         //     109.8 / 100.4 us; from the owning wave's substitution
@@ -572,8 +575,10 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
         //   pairs), not the tokens' 2-byte elements: 112.0 against 103.5 us.
         // With the row's stores skipped (wrong results, timing only) the step
         // takes 100.6 us and without the substitution 103.1: the 2.7 us left
-        // over the attention is the stores themselves.
-        if (k_new != nullptr && blockIdx.y == 0) {
+        // over the attention is the stores themselves.  Issued by the combine
+        // launch instead they still cost 2.2 us: each V element is a 2-byte
+        // write into a different 32-byte row of the [d][16] tile.
+        if (append_row && blockIdx.y == 0) {
             if (blockIdx.x % num_kv_heads == 0)
                 append_new_tokens<QT, D>(reinterpret_cast<QT *>(k_pool), reinterpret_cast<QT *>(v_pool),
                                          k_new, v_new, block_tables, ctx_lens, blockIdx.x / num_kv_heads,
@@ -1609,11 +1614,42 @@ constexpr int kCombineBatch = 8;
 
 // DPL dims per lane: head dim D <= 64 * DPL (dims past D are read clamped and
 // never stored).
+// Fused decode step over f16 / bf16 pools: the new tokens' K and V are
+// stored into the pools by the combine launch, which runs after every
+// partition work-group has read them from k_new / v_new in registers and
+// has memory bandwidth to spare.  16-bit elements are copied as bits.
+struct NewTokens {
+    uint16_t *k_pool, *v_pool;
+    const uint16_t *k_new, *v_new;  // null: nothing to store
+    const int32_t *tables;
+    int max_blocks, num_kv_heads, gqa, nq;
+    int64_t num_blocks;
+};
+
+// Wave-wide store of query token j's K and V for kv head kvh of sequence seq
+// (position ctx - nq + j; K [blk][Hkv][d/8][16][8], V [blk][Hkv][d][16]; a
+// block id outside the pool is skipped), the bits dlmk_kv_append writes.
+__device__ __forceinline__ void store_new_token(const NewTokens &nt, int seq, int j, int kvh, int ctx,
+                                                int D, int lane) {
+    const int p = ctx - nt.nq + j;
+    if (p < 0) return;
+    const int64_t blk = nt.tables[(int64_t)seq * nt.max_blocks + p / kBlock];
+    if (blk < 0 || blk >= nt.num_blocks) return;
+    const int t = p % kBlock;
+    const int64_t base = (blk * nt.num_kv_heads + kvh) * (int64_t)D * kBlock;
+    const int64_t src = ((int64_t)(seq * nt.nq + j) * nt.num_kv_heads + kvh) * D;
+    typedef uint32_t w4t __attribute__((ext_vector_type(4)));
+    for (int c = lane; c < D / 8; c += 64)
+        pool_store(reinterpret_cast<w4t *>(&nt.k_pool[base + (c * kBlock + t) * 8]),
+                   *reinterpret_cast<const w4t *>(&nt.k_new[src + 8 * c]));
+    for (int e = lane; e < D; e += 64) pool_store(&nt.v_pool[base + e * kBlock + t], nt.v_new[src + e]);
+}
+
 template <int DPL>
 __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wave_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
     const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
-    int max_blocks, int partition, int max_parts, int D) {
+    int max_blocks, int partition, int max_parts, int D, NewTokens nt) {
     constexpr int B = kCombineBatch;  // partitions loaded per batch
     // One wave per (sequence, query row), kCombineWaves rows per work-group:
     // the wave folds all of the row's partitions itself (online rescale), so
@@ -1643,6 +1679,12 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wave_ke
     load(0, max_parts - 1);
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
     const int nparts = parts_of(ctx, partition);
+    if (nt.k_new != nullptr) {
+        // Row r = j * Hq + h: the first row of each kv head's group stores
+        // that head's token j.
+        const int hq = nt.num_kv_heads * nt.gqa, h = r % hq;
+        if (h % nt.gqa == 0) store_new_token(nt, seq, r / hq, h / nt.gqa, ctx, D, lane);
+    }
     if (nparts == 1) return;
 
     float m = -INFINITY, L = 0.f, O[DPL];
@@ -1678,7 +1720,7 @@ template <int DPL>
 __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kernel(
     void *__restrict__ out, int out_dtype, const float *__restrict__ ws_o,
     const float *__restrict__ ws_ml, const int32_t *__restrict__ ctx_lens, int rows_per_seq,
-    int max_blocks, int partition, int max_parts, int D) {
+    int max_blocks, int partition, int max_parts, int D, NewTokens nt) {
     constexpr int W = kCombineWaves;
     __shared__ float wml[W][2];
     __shared__ float so[W][64 * DPL + 1];
@@ -1712,6 +1754,10 @@ __global__ __launch_bounds__(64 * kCombineWaves) void paged_attn_combine_wg_kern
     load(wave, max_parts - 1);
     const int ctx = min(ctx_lens[seq], max_blocks * kBlock);
     const int nparts = parts_of(ctx, partition);
+    if (nt.k_new != nullptr && wave == 0) {
+        const int r = blockIdx.x, hq = nt.num_kv_heads * nt.gqa, h = r % hq;
+        if (h % nt.gqa == 0) store_new_token(nt, seq, r / hq, h / nt.gqa, ctx, D, lane);
+    }
     if (nparts == 1) return;
     for (int p0 = wave;;) {
 #pragma unroll
@@ -1765,7 +1811,8 @@ inline int64_t parts_for(int max_blocks, int partition) {
 
 // Combine launch for DPL dims per lane (head dim <= 64 * DPL).
 template <int DPL>
-void launch_combine(const Args &a, int partition, int max_parts, float *ws_o, float *ws_ml) {
+void launch_combine(const Args &a, int partition, int max_parts, float *ws_o, float *ws_ml,
+                    const NewTokens &nt) {
     // Rows of up to kCombineBatch partitions: a wave per row (config 5
     // 64.9 -> 66.2%); longer rows: a work-group per row, whose four waves
     // share the row's partitions (the wave-per-row kernel was 0.8 points
@@ -1774,19 +1821,22 @@ void launch_combine(const Args &a, int partition, int max_parts, float *ws_o, fl
     if (max_parts > kCombineBatch)
         hipLaunchKernelGGL(paged_attn_combine_wg_kernel<DPL>, dim3((unsigned)(a.NQ * a.Hq), (unsigned)a.B),
                            dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
-                           a.NQ * a.Hq, a.max_blocks, partition, max_parts, a.D);
+                           a.NQ * a.Hq, a.max_blocks, partition, max_parts, a.D, nt);
     else
         hipLaunchKernelGGL(paged_attn_combine_wave_kernel<DPL>,
                            dim3((unsigned)((a.NQ * a.Hq + kCombineWaves - 1) / kCombineWaves), (unsigned)a.B),
                            dim3(64 * kCombineWaves), 0, a.stream, a.out, a.out_dtype, ws_o, ws_ml, a.ctx_lens,
-                           a.NQ * a.Hq, a.max_blocks, partition, max_parts, a.D);
+                           a.NQ * a.Hq, a.max_blocks, partition, max_parts, a.D, nt);
 }
 
 // Launches the partition kernel through `launch(grid, max_parts, ws_o, ws_ml)`
 // over grid_x x max_parts work-groups, then the combine kernel when a
 // sequence can span several partitions.
+// combine_appends: a fused decode step whose partition launch has no append
+// row when it is followed by a combine launch; the combine stores the new
+// tokens instead.
 template <typename Launch>
-int launch_pair(const Args &a, int partition, int64_t grid_x, Launch launch) {
+int launch_pair(const Args &a, int partition, int64_t grid_x, Launch launch, bool combine_appends = false) {
     const int max_parts = (int)parts_for(a.max_blocks, partition);
     float *ws_o = nullptr, *ws_ml = nullptr;
     if (grid_x > 0x7fffffff)
@@ -1806,11 +1856,16 @@ int launch_pair(const Args &a, int partition, int64_t grid_x, Launch launch) {
     }
     launch(dim3((unsigned)grid_x, (unsigned)max_parts), max_parts, ws_o, ws_ml);
     if (max_parts > 1) {
+        NewTokens nt{};
+        if (combine_appends && a.k_new != nullptr)
+            nt = NewTokens{static_cast<uint16_t *>(a.k_pool), static_cast<uint16_t *>(a.v_pool),
+                           static_cast<const uint16_t *>(a.k_new), static_cast<const uint16_t *>(a.v_new),
+                           a.tables, a.max_blocks, a.Hkv, a.Hq / a.Hkv, a.NQ, a.num_blocks};
         switch ((a.D + 63) / 64) {
-            case 1: launch_combine<1>(a, partition, max_parts, ws_o, ws_ml); break;
-            case 2: launch_combine<2>(a, partition, max_parts, ws_o, ws_ml); break;
-            case 3: launch_combine<3>(a, partition, max_parts, ws_o, ws_ml); break;
-            default: launch_combine<4>(a, partition, max_parts, ws_o, ws_ml); break;
+            case 1: launch_combine<1>(a, partition, max_parts, ws_o, ws_ml, nt); break;
+            case 2: launch_combine<2>(a, partition, max_parts, ws_o, ws_ml, nt); break;
+            case 3: launch_combine<3>(a, partition, max_parts, ws_o, ws_ml, nt); break;
+            default: launch_combine<4>(a, partition, max_parts, ws_o, ws_ml, nt); break;
         }
     }
     hipError_t e = hipGetLastError();
@@ -1838,15 +1893,17 @@ int launch_mfma_nb(const Args &a) {
                                a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
             return;
         }
-        // Fused decode step: one more grid row of append work-groups.
-        if (!C::kScaled && a.k_new != nullptr) grid.y += 1;
+        // Fused decode step: the new tokens are stored by the combine launch
+        // when there is one, else by one more grid row of append work-groups.
+        const int append_row = !C::kScaled && a.k_new != nullptr && max_parts == 1;
+        if (append_row) grid.y += 1;
         hipLaunchKernelGGL((paged_attn_mfma_kernel<C, D, GQA, NQ, NW, NB, PD>), grid, dim3(NW * 64), 0,
                            a.stream, a.out, a.out_dtype, static_cast<const QT *>(a.q),
                            static_cast<uint8_t *>(a.k_pool), static_cast<uint8_t *>(a.v_pool),
                            a.k_scales, a.v_scales, static_cast<const QT *>(a.k_new),
                            static_cast<const QT *>(a.v_new), a.tables, a.ctx_lens, a.Hq, a.Hkv,
-                           a.max_blocks, a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml);
-    });
+                           a.max_blocks, a.num_blocks, a.scale * kLog2e, max_parts, ws_o, ws_ml, append_row);
+    }, !C::kScaled && a.k_new != nullptr);
 }
 
 // Partition shape per launch.  f16 / bf16 and int8 pools: 16 blocks per wave
