@@ -224,8 +224,11 @@ int dlmk_paged_decode_attention(void *stream, void *out, int out_dtype, const vo
                                 void *workspace, size_t workspace_bytes);
 
 /* Fused decode step: appends each sequence's num_q_per_seq newest tokens and
- * runs dlmk_paged_decode_attention over them in one launch (the reference does
- * the two back to back inside dlm_decode_block, kernels.cu:361-366).
+ * runs dlmk_paged_decode_attention over them in the same launches, with no
+ * separate append kernel (the reference does the two back to back inside
+ * dlm_decode_block, kernels.cu:361-366): the attention reads the new tokens
+ * from k_new / v_new, and the pools are written by the split-K combine
+ * launch, or by the partition launch when there is no combine.
  * k_new / v_new are [num_seqs][num_q_per_seq][num_kv_heads][head_dim] in the
  * pool dtype; token j of sequence s goes to position ctx_lens[s] -
  * num_q_per_seq + j through block_tables (so ctx_lens already counts them and
