@@ -227,19 +227,31 @@ __device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][D],
         rowML[r][1] = L;
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < ROWS * D; idx += NW * 64) {
-        const int r = idx / D, d = idx - r * D;
-        float O = 0.f;
+    // Four consecutive dims per thread: 16-byte LDS reads and partial stores.
+    static_assert(D % 4 == 0, "float4 merge");
+    for (int idx = threadIdx.x; idx < ROWS * D / 4; idx += NW * 64) {
+        const int r = idx / (D / 4), d = 4 * (idx - r * (D / 4));
+        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
 #pragma unroll
-        for (int w = 0; w < NW; ++w) O = fmaf(fac[r][w], o_lds[w][r][d], O);
+        for (int w = 0; w < NW; ++w) {
+            const float4 v = *reinterpret_cast<const float4 *>(&o_lds[w][r][d]);
+            const float f = fac[r][w];
+            O.x = fmaf(f, v.x, O.x);
+            O.y = fmaf(f, v.y, O.y);
+            O.z = fmaf(f, v.z, O.z);
+            O.w = fmaf(f, v.w, O.w);
+        }
         const float L = rowML[r][1];
         const int j = r / GQA, h = kvh * GQA + r % GQA;
         const int64_t row = (int64_t)(seq * NQ + j) * num_q_heads + h;
         if (nparts == 1) {
-            store_out(out, out_dtype, row * D + d, L > 0.f ? O / L : 0.f);
+            store_out(out, out_dtype, row * D + d, L > 0.f ? O.x / L : 0.f);
+            store_out(out, out_dtype, row * D + d + 1, L > 0.f ? O.y / L : 0.f);
+            store_out(out, out_dtype, row * D + d + 2, L > 0.f ? O.z / L : 0.f);
+            store_out(out, out_dtype, row * D + d + 3, L > 0.f ? O.w / L : 0.f);
         } else {
             const int64_t slot = row * max_parts + part;
-            ws_o[slot * D + d] = O;
+            *reinterpret_cast<float4 *>(&ws_o[slot * D + d]) = O;
             if (d == 0) {
                 ws_ml[2 * slot] = rowML[r][0];
                 ws_ml[2 * slot + 1] = L;
@@ -542,7 +554,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     constexpr int64_t TILE = C::kTileBytes;  // bytes per (block, kv head)
     static_assert(ROWS <= 16 && D % 32 == 0, "unsupported geometry");
 
-    __shared__ float o_lds[NW][ROWS][D];
+    __shared__ __attribute__((aligned(16))) float o_lds[NW][ROWS][D];
     __shared__ float ml_lds[NW][ROWS][2];
 
     // blockIdx.x = seq * num_kv_heads + kv head, blockIdx.y = partition: the
@@ -994,7 +1006,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_packed_ker
     constexpr int P = NW * NB * kBlock;
     constexpr int64_t TILE = C::kTileBytes;
 
-    __shared__ float o_lds[NW][ROWS][D];
+    __shared__ __attribute__((aligned(16))) float o_lds[NW][ROWS][D];
     __shared__ float ml_lds[NW][ROWS][2];
     // Q rows in operand order, then one zero line.  Rows are padded by 16
     // bytes: at D * 2 bytes apart (a multiple of the 256-byte bank cycle) the
