@@ -183,6 +183,33 @@ def test_paged_attention_matches_oracle(oracle, torch_mod, ops, cuda, dtype, Hq,
         assert_close(got16, ref, atol, rtol, f"{name} out")
 
 
+@pytest.mark.parametrize("dtype,d,nq", [(np.float16, 128, 1), (np.float16, 128, 4),
+                                         (np.float32, 64, 1), (np.float32, 128, 1)])
+def test_paged_attention_masks_out_of_pool_blocks(oracle, torch_mod, ops, cuda, dtype, d, nq):
+    """A block id outside the pool inside the context is masked: the output equals
+    attention over the same sequence with that block removed."""
+    name = np.dtype(dtype).name
+    banner(f"attention {name} out-of-pool table ids d={d} nq={nq}")
+    rng = np.random.default_rng(33 + d + nq)
+    w = make_workload(rng, [700, 1300, 90, 2100], 32, 8, d, dtype, nq=nq,
+                      sigma=1.0 if dtype is np.float32 else 0.5)
+    nb = w.k_pool.shape[0]
+    tables = w.tables.copy()
+    bad = tables.copy()
+    ref_ctx = np.asarray(w.ctx, np.int32).copy()
+    for s, (bi, bad_id) in {0: (3, -1), 1: (40, nb + 5), 3: (0, 2**30)}.items():
+        bad[s, bi] = bad_id
+        row = np.delete(tables[s], bi)
+        tables[s] = np.concatenate([row, row[-1:]])
+        ref_ctx[s] -= 16
+    ref = oracle.paged_attention(w.q, w.k_pool, w.v_pool, tables, ref_ctx, w.nq, w.Hq, w.Hkv,
+                                 w.d, w.bs, w.scale)
+    w.tables = bad
+    got = run_attention(torch_mod, ops, cuda, w, out_dtype=torch_mod.float32)
+    atol, rtol = (F16_ATOL, F16_RTOL) if dtype is np.float16 else (F32_ATOL, F32_RTOL)
+    assert_close(got, ref, atol, rtol, f"{name} masked blocks")
+
+
 def test_paged_attention_ignores_stale_block_tails(oracle, torch_mod, ops, cuda):
     """Slots past the context (and past a verify query's limit) may hold NaN."""
     banner("attention stale NaN tails")

@@ -311,3 +311,39 @@ def test_fork_quant_pools(oracle, torch_mod, ops, cuda, qname):
     for a in (kp, vp, ksc, vsc):
         a[20:30] = a[0:10]
     assert_pools_equal(kv, kp, vp, ksc, vsc, f"fork {qname}")
+
+
+@pytest.mark.parametrize("qname", ["int8", "int4"])
+@pytest.mark.parametrize("Hq,nq", [(32, 1), (32, 2), (32, 4)])  # 4 / 8 / 16 rows
+def test_attention_quant_masks_out_of_pool_blocks(oracle, torch_mod, ops, cuda, qname, Hq, nq):
+    """A block id outside the pool (negative or >= num_blocks) inside the context is
+    masked: the output equals attention over the same sequence with that block
+    removed (the remaining tokens keep their order; the causal limits of the last
+    nq positions are unchanged), and nothing outside the pool is read."""
+    torch = torch_mod
+    banner(f"attention_quant {qname} out-of-pool table ids Hq={Hq} nq={nq}")
+    quant = _quant(oracle, qname)
+    Hkv, d = 8, 128
+    ctx = [700, 1300, 90, 2100]
+    rng = np.random.default_rng(77 + nq)
+    kp, vp, ksc, vsc, tables = quant_workload(oracle, rng, ctx, Hkv, d, quant)
+    nb = kp.shape[0]
+    bad = tables.copy()
+    ref_tables = tables.copy()
+    ref_ctx = np.asarray(ctx, np.int32).copy()
+    for s, (bi, bad_id) in {0: (3, -1), 1: (40, nb + 5), 3: (0, 2**30)}.items():
+        bad[s, bi] = bad_id
+        row = np.delete(tables[s], bi)
+        ref_tables[s] = np.concatenate([row, row[-1:]])
+        ref_ctx[s] -= BS
+    q = rng.standard_normal((len(ctx), nq, Hq, d)).astype(np.float16)
+    scale = np.float32(1.0) / np.sqrt(np.float32(d))
+    ref = oracle.paged_attention_quant(q.astype(np.float32), kp, vp, ksc, vsc, quant, ref_tables,
+                                       ref_ctx, nq, Hq, Hkv, d, scale)
+    kv = upload(torch, ops, cuda, kp, vp, ksc, vsc, qname)
+    out = ops.paged_decode_attention_quant(
+        to_dev(torch, q, cuda), kv, to_dev(torch, bad, cuda),
+        to_dev(torch, np.asarray(ctx, np.int32), cuda), num_kv_heads=Hkv, scale=float(scale),
+        out_dtype=torch.float32)
+    torch.cuda.synchronize()
+    assert_close(out.cpu().numpy(), ref, F16_ATOL, F16_RTOL, f"attention {qname} masked blocks")
