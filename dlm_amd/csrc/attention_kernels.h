@@ -32,8 +32,13 @@
 //     the B operand is 4 tokens x 1 dim = 8 contiguous bytes of the V tile
 //     [d][16].
 // int8 / int4 pools: the same kernel over f16 operands widened in registers
-//   from tiles laid out for 16-byte loads per lane (storage codecs below).
-// f32 pools: VALU kernel (dot products with FMA, cross-lane sums).
+//   from tiles laid out for 16-byte loads per lane (storage codecs below);
+//   query groups of up to 4 rows (int4: 8) run paged_attn_packed_kernel,
+//   which puts 4 (2) blocks into one score tile instead of padding it with
+//   zero query rows.
+// f32 pools, and geometries the tuned kernels are not instantiated for:
+//   paged_attn_generic_kernel, the same tiling with the head dim, GQA group
+//   and query count at run time (f32 on v_mfma_f32_16x16x4_f32).
 
 #include <hip/hip_runtime.h>
 
