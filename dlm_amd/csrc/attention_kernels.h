@@ -207,8 +207,9 @@ __device__ __forceinline__ int parts_of(int ctx, int P) { return ctx > P ? (ctx 
 // finish the rows (single-partition sequence) or store the partition partial.
 // The ROWS x NW merge weights 2^(m_w - M) are computed once into LDS, so the
 // per-element pass is a plain weighted sum of the waves' O.
-template <int ROWS, int D, int NW, int GQA, int NQ>
-__device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][D],
+// o_lds rows may be padded (DS > D) to keep the waves' stores conflict-free.
+template <int ROWS, int D, int NW, int GQA, int NQ, int DS>
+__device__ __forceinline__ void merge_waves(const float (&o_lds)[NW][ROWS][DS],
                                             const float (&ml_lds)[NW][ROWS][2], void *out,
                                             int out_dtype, int seq, int kvh, int part,
                                             int nparts, int num_q_heads, int max_parts,
@@ -559,7 +560,9 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_mfma_kerne
     constexpr int64_t TILE = C::kTileBytes;  // bytes per (block, kv head)
     static_assert(ROWS <= 16 && D % 32 == 0, "unsupported geometry");
 
-    __shared__ __attribute__((aligned(16))) float o_lds[NW][ROWS][D];
+    // Rows padded by 16 bytes: rows D * 4 bytes apart sit in the same LDS banks,
+    // and the epilogue's stores write several rows per instruction.
+    __shared__ __attribute__((aligned(16))) float o_lds[NW][ROWS][D + 4];
     __shared__ float ml_lds[NW][ROWS][2];
 
     // blockIdx.x = seq * num_kv_heads + kv head, blockIdx.y = partition: the
@@ -1011,7 +1014,9 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_packed_ker
     constexpr int P = NW * NB * kBlock;
     constexpr int64_t TILE = C::kTileBytes;
 
-    __shared__ __attribute__((aligned(16))) float o_lds[NW][ROWS][D];
+    // Rows padded by 16 bytes: rows D * 4 bytes apart sit in the same LDS banks,
+    // and the epilogue's stores write several rows per instruction.
+    __shared__ __attribute__((aligned(16))) float o_lds[NW][ROWS][D + 4];
     __shared__ float ml_lds[NW][ROWS][2];
     // Q rows in operand order, then one zero line.  Rows are padded by 16
     // bytes: at D * 2 bytes apart (a multiple of the 256-byte bank cycle) the
