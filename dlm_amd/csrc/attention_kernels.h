@@ -1348,7 +1348,8 @@ __global__ __launch_bounds__(NW * 64) void paged_attn_generic_kernel(
     static_assert(DP % (4 * X) == 0 && DP % 16 == 0, "unsupported padded head dim");
     static_assert(NW >= 2, "new-token blocks must land on different waves");
 
-    __shared__ float o_lds[NW][16][DP];
+    // Rows padded by 16 bytes: the epilogue stores 4 rows per instruction.
+    __shared__ __attribute__((aligned(16))) float o_lds[NW][16][DP + 4];
     __shared__ float ml_lds[NW][16][2];
 
     const int hd = geo.hd, gqa = geo.gqa, nq = geo.nq;
