@@ -1003,6 +1003,7 @@ __global__ __launch_bounds__(NW * 64) DLMK_MFMA_ATTRS void paged_attn_packed_ker
     constexpr int G = 4 / T;               // lane groups per block
     constexpr int NG = NB / T;             // block groups per wave
     static_assert(NB % T == 0, "blocks per wave must fill the block groups");
+    static_assert(NB <= 32, "block validity is a 32-bit mask");
     constexpr int CH = D / 8 / G;          // 8-dim chunks a lane group feeds per block = QK steps per group
     constexpr int SK = C::KG / 8;          // chunks per K load
     constexpr int NLK = CH / SK;           // K loads per lane per group
