@@ -733,10 +733,12 @@ def main():
             "bound": "hbm", "achieved": round(attn_gbps, 1), "peak": HBM_PEAK_GBPS,
             "unit": "GB/s", "frac": round(attn_gbps / HBM_PEAK_GBPS, 4), "traffic": traffic,
             # Quantized pools with GQA groups of up to 4 rows (int4: 8) run the
-            # packed kernel (several blocks per score tile).
+            # packed kernel (several blocks per score tile); int8 only for rows
+            # of up to 4 partitions of 1024 tokens.
             "kernel": ("paged_attn_generic_kernel" if w.dtype == "f32" else
                        "paged_attn_packed_kernel" if (w.quant == "int4" and w.hq // w.hkv * w.nq <= 8)
-                       or (w.quant == "int8" and w.hq // w.hkv * w.nq <= 4) else "paged_attn_mfma_kernel"),
+                       or (w.quant == "int8" and w.hq // w.hkv * w.nq <= 4 and w.ctx[1] <= 4096)
+                       else "paged_attn_mfma_kernel"),
             "traffic_detail": traffic_note,
         },
     }

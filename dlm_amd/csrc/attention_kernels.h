@@ -129,6 +129,12 @@ constexpr float kLog2e = 1.4426950408889634f;
 #ifndef DLMK_MFMA_PACKED
 #define DLMK_MFMA_PACKED 3
 #endif
+// int8 rows of more than this many partitions take the unpacked kernel:
+// configs[2] (rows up to 8704 tokens, 9 partitions) 66.1 -> 67.2% of HBM peak
+// that way; configs[1] (4 partitions) keeps the packed kernel's 67.7%.
+#ifndef DLMK_PACKED_I8_MAXPARTS
+#define DLMK_PACKED_I8_MAXPARTS 4
+#endif
 // Blocks per wave for int8 pools.
 #ifndef DLMK_MFMA_Q8NB
 #define DLMK_MFMA_Q8NB 16
@@ -1909,7 +1915,8 @@ int launch_mfma_nb(const Args &a) {
     return launch_pair(a, NW * NB * kBlock, (int64_t)a.B * a.Hkv,
                        [&](dim3 grid, int max_parts, float *ws_o, float *ws_ml) {
         constexpr int kPackBit = C::kCodeBits == 4 ? 1 : GQA * NQ <= 4 ? 2 : 4;
-        if constexpr (C::kScaled && GQA * NQ <= 8 && (DLMK_MFMA_PACKED & kPackBit)) {
+        const bool pack_rows = C::kCodeBits == 4 || max_parts <= DLMK_PACKED_I8_MAXPARTS;
+        if constexpr (C::kScaled && GQA * NQ <= 8 && (DLMK_MFMA_PACKED & kPackBit)) if (pack_rows) {
             constexpr int PDP = GQA * NQ <= 4 ? DLMK_MFMA_PDP4 : DLMK_MFMA_PDP2;
             hipLaunchKernelGGL((paged_attn_packed_kernel<C, D, GQA, NQ, NW, NB, PDP>), grid, dim3(NW * 64), 0,
                                a.stream, a.out, a.out_dtype, static_cast<const QT *>(a.q),
